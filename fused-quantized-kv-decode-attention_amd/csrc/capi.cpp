@@ -1,0 +1,300 @@
+// extern "C" entry points of libfqkv_decode.so (declared in include/fqkv_decode.h).
+//
+// Each entry point validates its arguments before touching the GPU, picks
+// the query-head group size and split count, and launches the partial
+// kernel (plus the combine kernel when the sequence is split) on the
+// caller's stream. Nothing here allocates device memory.
+#include <hip/hip_runtime.h>
+#include <limits.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include <atomic>
+
+#include "fqkv_decode.h"
+#include "kv_formats.h"
+#include "launch.h"
+
+using namespace fqkv;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(FQKV_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
+
+// CU count per device, queried once (256 on MI355X).
+constexpr int MAX_DEV = 64;
+std::atomic<int> g_cus[MAX_DEV];
+
+int device_cus(int* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= MAX_DEV) return fail(FQKV_ERR_HIP, "device index %d out of range", dev);
+  int c = g_cus[dev].load(std::memory_order_relaxed);
+  if (c <= 0) {
+    e = hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute");
+    g_cus[dev].store(c, std::memory_order_relaxed);
+  }
+  *out = c;
+  return FQKV_OK;
+}
+
+int choose_hg(int64_t G, int fmt) {
+  if (fmt != KV_F16) return 1;
+  if (G <= 1) return 1;
+  if (G == 2) return 2;
+  if (G <= 4) return 4;
+  return 8;
+}
+
+// Splits for the single-block entry points: enough workgroups for about two
+// per CU, but at least two 16-token tiles per wave in every split.
+int64_t splits_for(int64_t rows, int64_t G, int64_t N, int fmt, int64_t W, int cus) {
+  const int hg = choose_hg(G, fmt);
+  const int64_t groups = rows * ((G + hg - 1) / hg);
+  const int64_t target = 2 * (int64_t)cus;
+  if (groups >= target) return 1;
+  int64_t S = (target + groups - 1) / groups;
+  const int64_t min_chunk = 32 * W;
+  const int64_t cap = N / min_chunk;
+  if (S > cap) S = cap;
+  return S < 1 ? 1 : S;
+}
+
+size_t scratch_bytes(int64_t heads, int64_t S, int64_t D) {
+  return (size_t)heads * (size_t)S * (size_t)(D + 2) * sizeof(float);
+}
+
+int check_common(int64_t N, int64_t D, int64_t W) {
+  if (N < 1 || N > INT_MAX - 1024) return fail(FQKV_ERR_ARG, "N: sequence length must be in [1, 2^31 - 1024), got %lld", (long long)N);
+  if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
+  if (W != 2 && W != 4 && W != 8) return fail(FQKV_ERR_ARG, "W: waves per workgroup must be 2, 4 or 8, got %lld", (long long)W);
+  return FQKV_OK;
+}
+
+// Single-block style decode: rows KV rows, G query heads per row. Splits the
+// sequence internally when rows alone cannot fill the GPU and the workspace allows.
+int run_decode(int fmt, const void* q, const void* K, const void* V, const void* Ks,
+               const void* Vs, void* o, int64_t rows, int64_t G, int64_t N, int64_t D, int64_t W,
+               void* ws, size_t ws_bytes, hipStream_t st) {
+  int cus = 0;
+  int rc = device_cus(&cus);
+  if (rc) return rc;
+  const int hg = choose_hg(G, fmt);
+  const int64_t ngroups = (G + hg - 1) / hg;
+  const int64_t heads = rows * G;
+  int64_t S = splits_for(rows, G, N, fmt, W, cus);
+  if (S > 1 && (ws == nullptr || scratch_bytes(heads, S, D) > ws_bytes)) {
+    const int64_t fit = ws ? (int64_t)(ws_bytes / scratch_bytes(heads, 1, D)) : 0;
+    S = fit >= 2 ? (fit < S ? fit : S) : 1;
+  }
+  if (S > 1 && !aligned(ws, 16)) return fail(FQKV_ERR_ARG, "workspace must be 16-byte aligned");
+  const int64_t nblocks = rows * ngroups * S;
+  if (nblocks > INT_MAX) return fail(FQKV_ERR_ARG, "problem too large: %lld workgroups", (long long)nblocks);
+
+  PartialParams p{};
+  p.q = (const _Float16*)q;
+  p.K = (const uint8_t*)K;
+  p.V = (const uint8_t*)V;
+  p.Ks = (const _Float16*)Ks;
+  p.Vs = (const _Float16*)Vs;
+  p.o = (_Float16*)o;
+  p.G = (int)G;
+  p.N = (int)N;
+  p.S = (int)S;
+  p.chunk = (int)((N + S - 1) / S);
+  p.ngroups = (int)ngroups;
+  p.scale = 1.0f / sqrtf((float)D);
+  p.c = p.scale * 1.4426950408889634f;
+  p.direct = S == 1;
+  if (!p.direct) {
+    float* f = (float*)ws;
+    p.m_part = f;
+    p.l_part = f + heads * S;
+    p.o_part = f + 2 * heads * S;
+  }
+  hipError_t e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)W, st);
+  if (e != hipSuccess) return hip_fail(e, "launch: partial kernel");
+  if (!p.direct) {
+    e = launch_combine((int)D, p.m_part, p.l_part, p.o_part, o, (int)heads, (int)S, 4, st);
+    if (e != hipSuccess) return hip_fail(e, "launch: combine kernel");
+  }
+  return FQKV_OK;
+}
+
+int check_ptrs_kv(const void* q, const void* K, const void* V, const void* o) {
+  if (!q || !K || !V || !o) return fail(FQKV_ERR_ARG, "null tensor pointer");
+  if (!aligned(K, 16) || !aligned(V, 16)) return fail(FQKV_ERR_ARG, "K and V must be 16-byte aligned");
+  if (!aligned(q, 2) || !aligned(o, 2)) return fail(FQKV_ERR_ARG, "q and o must be 2-byte aligned");
+  return FQKV_OK;
+}
+
+int sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l_part,
+            float* o_part, void* o, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int64_t S,
+            int64_t W, int64_t CW, void* stream, void* ev_begin, void* ev_end) {
+  int rc = check_common(N, D, W);
+  if (rc) return rc;
+  if (CW != 4 && CW != 8) return fail(FQKV_ERR_ARG, "CW: combine waves must be 4 or 8, got %lld", (long long)CW);
+  if (S < 1 || S > (1 << 20)) return fail(FQKV_ERR_ARG, "S: split count must be in [1, 2^20], got %lld", (long long)S);
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
+    return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
+  rc = check_ptrs_kv(q, K, V, o);
+  if (rc) return rc;
+  if (!m_part || !l_part || !o_part) return fail(FQKV_ERR_ARG, "null scratch pointer");
+  if (!aligned(o_part, 8)) return fail(FQKV_ERR_ARG, "o_part must be 8-byte aligned");
+  const int64_t G = Hq / Hkv;
+  const int hg = choose_hg(G, KV_F16);
+  const int64_t ngroups = (G + hg - 1) / hg;
+  const int64_t nblocks = Hkv * ngroups * S;
+  if (nblocks > INT_MAX || Hq > INT_MAX) return fail(FQKV_ERR_ARG, "problem too large");
+  hipStream_t st = (hipStream_t)stream;
+
+  PartialParams p{};
+  p.q = (const _Float16*)q;
+  p.K = (const uint8_t*)K;
+  p.V = (const uint8_t*)V;
+  p.m_part = m_part;
+  p.l_part = l_part;
+  p.o_part = o_part;
+  p.G = (int)G;
+  p.N = (int)N;
+  p.S = (int)S;
+  p.chunk = (int)((N + S - 1) / S);
+  p.ngroups = (int)ngroups;
+  p.scale = 1.0f / sqrtf((float)D);
+  p.c = p.scale * 1.4426950408889634f;
+  p.direct = 0;
+  hipError_t e;
+  if (ev_begin && (e = hipEventRecord((hipEvent_t)ev_begin, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+  e = launch_partial(KV_F16, (int)D, hg, p, (int)nblocks, (int)W, st);
+  if (e != hipSuccess) return hip_fail(e, "partial");
+  if (ev_end && (e = hipEventRecord((hipEvent_t)ev_end, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
+  e = launch_combine((int)D, m_part, l_part, o_part, o, (int)Hq, (int)S, (int)CW, st);
+  if (e != hipSuccess) return hip_fail(e, "combine");
+  return FQKV_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fqkv_last_error(void) { return g_err; }
+
+const char* fqkv_version(void) { return "fqkv_decode 0.1.0 (gfx950)"; }
+
+int fqkv_device_cu_count(int* cu_count) {
+  if (!cu_count) return fail(FQKV_ERR_ARG, "null cu_count");
+  return device_cus(cu_count);
+}
+
+int64_t fqkv_choose_splits(int64_t rows, int64_t G, int64_t N, int64_t D, int kv_format, int64_t W) {
+  (void)D;
+  int cus = 256;
+  if (device_cus(&cus) != FQKV_OK) cus = 256;
+  if (rows < 1 || G < 1 || N < 1) return 1;
+  return splits_for(rows, G, N, kv_format, W, cus);
+}
+
+size_t fqkv_workspace_bytes(int64_t rows, int64_t G, int64_t N, int64_t D, int kv_format, int64_t W) {
+  const int64_t S = fqkv_choose_splits(rows, G, N, D, kv_format, W);
+  return S > 1 ? scratch_bytes(rows * G, S, D) : 0;
+}
+
+int fqkv_decode_attn_fp16_mw(const void* q, const void* K, const void* V, void* o, int64_t B,
+                             int64_t N, int64_t D, int64_t W, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  int rc = check_common(N, D, W);
+  if (rc) return rc;
+  if (B < 1) return fail(FQKV_ERR_ARG, "B: batch must be >= 1, got %lld", (long long)B);
+  if ((rc = check_ptrs_kv(q, K, V, o))) return rc;
+  return run_decode(KV_F16, q, K, V, nullptr, nullptr, o, B, 1, N, D, W, workspace, workspace_bytes,
+                    (hipStream_t)stream);
+}
+
+static int quant_entry(int fmt, const void* q, const void* K, const void* V, const void* Ks,
+                       const void* Vs, void* o, int64_t B, int64_t N, int64_t D, int64_t W,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_common(N, D, W);
+  if (rc) return rc;
+  if (B < 1) return fail(FQKV_ERR_ARG, "B: batch must be >= 1, got %lld", (long long)B);
+  if (!q || !K || !V || !Ks || !Vs || !o) return fail(FQKV_ERR_ARG, "null tensor pointer");
+  const uintptr_t kal = (fmt == KV_I4 && D == 64) ? 8 : 16;
+  if (!aligned(K, kal) || !aligned(V, kal)) return fail(FQKV_ERR_ARG, "K and V must be %d-byte aligned", (int)kal);
+  if (!aligned(q, 2) || !aligned(o, 2) || !aligned(Ks, 2) || !aligned(Vs, 2))
+    return fail(FQKV_ERR_ARG, "q, o and scales must be 2-byte aligned");
+  return run_decode(fmt, q, K, V, Ks, Vs, o, B, 1, N, D, W, workspace, workspace_bytes,
+                    (hipStream_t)stream);
+}
+
+int fqkv_decode_attn_int8_mw(const void* q, const void* K, const void* V, const void* Ks,
+                             const void* Vs, void* o, int64_t B, int64_t N, int64_t D,
+                             int64_t W, void* workspace, size_t workspace_bytes, void* stream) {
+  return quant_entry(KV_I8, q, K, V, Ks, Vs, o, B, N, D, W, workspace, workspace_bytes, stream);
+}
+
+int fqkv_decode_attn_int4(const void* q, const void* K, const void* V, const void* Ks,
+                          const void* Vs, void* o, int64_t B, int64_t N, int64_t D, int64_t W,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  return quant_entry(KV_I4, q, K, V, Ks, Vs, o, B, N, D, W, workspace, workspace_bytes, stream);
+}
+
+int fqkv_decode_attn_gqa(const void* q, const void* K, const void* V, void* o, int64_t B,
+                         int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int64_t W,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_common(N, D, W);
+  if (rc) return rc;
+  if (B < 1) return fail(FQKV_ERR_ARG, "B: batch must be >= 1, got %lld", (long long)B);
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
+    return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
+  if ((rc = check_ptrs_kv(q, K, V, o))) return rc;
+  return run_decode(KV_F16, q, K, V, nullptr, nullptr, o, B * Hkv, Hq / Hkv, N, D, W, workspace,
+                    workspace_bytes, (hipStream_t)stream);
+}
+
+int fqkv_gqa_sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l_part,
+                     float* o_part, void* o, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                     int64_t S, int64_t W, int64_t CW, void* stream) {
+  return sk_fast(q, K, V, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW, stream, nullptr, nullptr);
+}
+
+int fqkv_gqa_sk_fast_timed(const void* q, const void* K, const void* V, float* m_part,
+                           float* l_part, float* o_part, void* o, int64_t Hq, int64_t Hkv,
+                           int64_t N, int64_t D, int64_t S, int64_t W, int64_t CW, void* stream,
+                           void* ev_begin, void* ev_end) {
+  return sk_fast(q, K, V, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW, stream, ev_begin, ev_end);
+}
+
+int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, int64_t D,
+                    int kv_format, int path, void* stream) {
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
+  if (path != 0 && path != 1) return fail(FQKV_ERR_ARG, "path must be 0 (K side) or 1 (V side)");
+  if (tokens < 1) return fail(FQKV_ERR_ARG, "tokens must be >= 1");
+  if (!Kq || !Ks || !out) return fail(FQKV_ERR_ARG, "null tensor pointer");
+  const uintptr_t kal = (kv_format == FQKV_KV_I4 && D == 64) ? 8 : 16;
+  if (!aligned(Kq, kal)) return fail(FQKV_ERR_ARG, "Kq must be %d-byte aligned", (int)kal);
+  if (!aligned(Ks, 2) || !aligned(out, 4)) return fail(FQKV_ERR_ARG, "misaligned scale or output pointer");
+  hipError_t e = launch_dequant(kv_format, (int)D, path, Kq, Ks, out, tokens, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "launch: dequant kernel");
+  return FQKV_OK;
+}
+
+}  // extern "C"

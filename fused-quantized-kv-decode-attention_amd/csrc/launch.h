@@ -1,0 +1,41 @@
+// Internal host <-> kernel interface of libfqkv_decode (not part of the C ABI).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fqkv {
+
+constexpr int NW_MAX = 8;  // waves per workgroup the kernels are sized for
+
+// Work item of the partial kernel: blockIdx.x = (r * ngroups + g) * S + s
+// with r the KV row (batch * kv_head), g the query-head group (HG heads of
+// the G query heads that share KV row r) and s the split.
+struct PartialParams {
+  const _Float16* q;     // [R * G, D]
+  const uint8_t* K;      // [R, N, row_bytes]
+  const uint8_t* V;      // [R, N, row_bytes]
+  const _Float16* Ks;    // [R, N] (int8 / int4 only)
+  const _Float16* Vs;    // [R, N]
+  _Float16* o;           // [R * G, D] when direct
+  float* m_part;         // [R * G, S] when !direct
+  float* l_part;         // [R * G, S]
+  float* o_part;         // [R * G, S, D]
+  int G;                 // query heads per KV row
+  int N;                 // tokens
+  int S;                 // splits
+  int chunk;             // ceil(N / S)
+  int ngroups;           // ceil(G / HG)
+  float c;               // softmax scale * log2(e)
+  float scale;           // softmax scale (natural-log units for m_part)
+  int direct;            // 1: S == 1, write normalised fp16 output
+};
+
+hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& p, int nblocks, int nw,
+                          hipStream_t st);
+hipError_t launch_combine(int D, const float* m_part, const float* l_part, const float* o_part,
+                          void* o, int H, int S, int nw, hipStream_t st);
+hipError_t launch_dequant(int fmt, int D, int path, const void* Kq, const void* Ks, float* out,
+                          int64_t tokens, hipStream_t st);
+
+}  // namespace fqkv

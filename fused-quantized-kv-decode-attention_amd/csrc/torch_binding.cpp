@@ -1,0 +1,256 @@
+// PyTorch binding of libfqkv_decode: the reference's extension call surface.
+//
+// Five functions with the reference's names, argument order, tensor layouts
+// and return conventions (kernels/decode_attn_fp16_mw.cu:50,64;
+// decode_attn_int8_mw.cu:52,65; decode_attn_int4.cu:47,58;
+// decode_attn_gqa.cu:56,69; decode_attn_gqa_sk_fast.cu:95,113). Validation
+// is a superset of the reference's TORCH_CHECKs: each message starts with
+// the reference's keyword ("cuda", "fp16", "contig", "D", "W", "int8",
+// "packed uint8", "CW", "partial", "combine", "launch"). Work is launched on
+// PyTorch's current HIP stream of the inputs' device (the reference used
+// the legacy default stream), so HIP graph capture and stream overlap work.
+#include <torch/extension.h>
+#include <c10/core/DeviceGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include "fqkv_decode.h"
+
+namespace {
+
+void check_rc(int rc, const char* tag) {
+  TORCH_CHECK(rc == FQKV_OK, tag, ": ", fqkv_last_error());
+}
+
+void* cur_stream(const torch::Tensor& t) {
+  return (void*)c10::hip::getCurrentHIPStream(t.get_device()).stream();
+}
+
+void check_gpu(std::initializer_list<const torch::Tensor*> ts) {
+  const torch::Tensor& first = **ts.begin();
+  for (const torch::Tensor* t : ts) {
+    TORCH_CHECK(t->is_cuda(), "cuda: all tensors must be on the GPU");
+    TORCH_CHECK(t->device() == first.device(), "cuda: all tensors must be on the same device");
+    TORCH_CHECK(t->is_contiguous(), "contig: all tensors must be contiguous");
+  }
+}
+
+void check_half(const torch::Tensor& t, const char* name) {
+  TORCH_CHECK(t.scalar_type() == torch::kHalf, "fp16: ", name, " must be float16");
+}
+
+void check_W(int64_t W) { TORCH_CHECK(W == 2 || W == 4 || W == 8, "W: must be 2, 4 or 8, got ", W); }
+
+void check_D(int64_t D) { TORCH_CHECK(D == 64 || D == 128, "D: head_dim must be 64 or 128, got ", D); }
+
+torch::Tensor workspace_for(const torch::Tensor& q, int64_t rows, int64_t G, int64_t N, int64_t D,
+                            int fmt, int64_t W) {
+  const c10::DeviceGuard guard(q.device());
+  const size_t bytes = fqkv_workspace_bytes(rows, G, N, D, fmt, W);
+  if (bytes == 0) return torch::Tensor();
+  return torch::empty({(int64_t)bytes}, q.options().dtype(torch::kUInt8));
+}
+
+// decode_attn_fp16_mw(q[B,D], K[B,N,D], V[B,N,D], W) -> o[B,D]
+torch::Tensor decode_attn_fp16_mw(torch::Tensor q, torch::Tensor K, torch::Tensor V, int64_t W) {
+  check_gpu({&q, &K, &V});
+  check_half(q, "q");
+  check_half(K, "K");
+  check_half(V, "V");
+  TORCH_CHECK(q.dim() == 2 && K.dim() == 3 && V.sizes() == K.sizes() && q.size(0) == K.size(0) &&
+                  q.size(1) == K.size(2),
+              "shape: expected q [B,D], K and V [B,N,D]; got q ", q.sizes(), ", K ", K.sizes(), ", V ", V.sizes());
+  const int64_t B = K.size(0), N = K.size(1), D = K.size(2);
+  check_D(D);
+  check_W(W);
+  TORCH_CHECK(N >= 1, "N: need at least one cached token");
+  const c10::DeviceGuard guard(q.device());
+  auto o = torch::empty({B, D}, q.options());
+  auto ws = workspace_for(q, B, 1, N, D, FQKV_KV_F16, W);
+  check_rc(fqkv_decode_attn_fp16_mw(q.data_ptr(), K.data_ptr(), V.data_ptr(), o.data_ptr(), B, N, D, W,
+                                    ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0,
+                                    cur_stream(q)),
+           "launch");
+  return o;
+}
+
+torch::Tensor quant_common(int fmt, torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks,
+                           torch::Tensor Vs, int64_t W) {
+  check_gpu({&q, &K, &V, &Ks, &Vs});
+  check_half(q, "q");
+  check_half(Ks, "Ks");
+  check_half(Vs, "Vs");
+  if (fmt == FQKV_KV_I8) {
+    TORCH_CHECK(K.scalar_type() == torch::kChar && V.scalar_type() == torch::kChar, "int8: K and V must be int8");
+  } else {
+    TORCH_CHECK(K.scalar_type() == torch::kByte && V.scalar_type() == torch::kByte,
+                "packed uint8: K and V must be uint8 holding two int4 values per byte");
+  }
+  TORCH_CHECK(q.dim() == 2 && K.dim() == 3 && V.sizes() == K.sizes() && q.size(0) == K.size(0),
+              "shape: expected q [B,D], K and V [B,N,", fmt == FQKV_KV_I8 ? "D" : "D/2", "]; got q ", q.sizes(),
+              ", K ", K.sizes(), ", V ", V.sizes());
+  const int64_t B = K.size(0), N = K.size(1);
+  const int64_t D = fmt == FQKV_KV_I8 ? K.size(2) : 2 * K.size(2);
+  if (fmt == FQKV_KV_I4) {
+    TORCH_CHECK(D == 64 || D == 128, "D: packed int4 rows must hold 32 or 64 bytes (head_dim 64 or 128), got ",
+                K.size(2), " bytes");
+  }
+  check_D(D);
+  TORCH_CHECK(q.size(1) == D, "shape: q head_dim ", q.size(1), " does not match KV head_dim ", D);
+  TORCH_CHECK(Ks.dim() == 2 && Ks.size(0) == B && Ks.size(1) == N && Vs.sizes() == Ks.sizes(),
+              "shape: expected per-token scales Ks and Vs [B,N]; got ", Ks.sizes(), " and ", Vs.sizes());
+  check_W(W);
+  TORCH_CHECK(N >= 1, "N: need at least one cached token");
+  const c10::DeviceGuard guard(q.device());
+  auto o = torch::empty({B, D}, q.options());
+  auto ws = workspace_for(q, B, 1, N, D, fmt, W);
+  void* wsp = ws.defined() ? ws.data_ptr() : nullptr;
+  const size_t wsb = ws.defined() ? ws.numel() : 0;
+  const int rc = fmt == FQKV_KV_I8
+                     ? fqkv_decode_attn_int8_mw(q.data_ptr(), K.data_ptr(), V.data_ptr(), Ks.data_ptr(),
+                                                Vs.data_ptr(), o.data_ptr(), B, N, D, W, wsp, wsb, cur_stream(q))
+                     : fqkv_decode_attn_int4(q.data_ptr(), K.data_ptr(), V.data_ptr(), Ks.data_ptr(),
+                                             Vs.data_ptr(), o.data_ptr(), B, N, D, W, wsp, wsb, cur_stream(q));
+  check_rc(rc, "launch");
+  return o;
+}
+
+// decode_attn_int8_mw(q[B,D], K[B,N,D] int8, V, Ks[B,N] fp16, Vs, W) -> o[B,D]
+torch::Tensor decode_attn_int8_mw(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks,
+                                  torch::Tensor Vs, int64_t W) {
+  return quant_common(FQKV_KV_I8, q, K, V, Ks, Vs, W);
+}
+
+// decode_attn_int4(q[B,D], K[B,N,D/2] uint8, V, Ks[B,N] fp16, Vs, W) -> o[B,D]
+torch::Tensor decode_attn_int4(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks,
+                               torch::Tensor Vs, int64_t W) {
+  return quant_common(FQKV_KV_I4, q, K, V, Ks, Vs, W);
+}
+
+// decode_attn_gqa(q[B,Hq,D], K[B,Hkv,N,D], V, W) -> o[B,Hq,D]
+torch::Tensor decode_attn_gqa(torch::Tensor q, torch::Tensor K, torch::Tensor V, int64_t W) {
+  check_gpu({&q, &K, &V});
+  check_half(q, "q");
+  check_half(K, "K");
+  check_half(V, "V");
+  TORCH_CHECK(q.dim() == 3 && K.dim() == 4 && V.sizes() == K.sizes() && q.size(0) == K.size(0) &&
+                  q.size(2) == K.size(3),
+              "shape: expected q [B,Hq,D], K and V [B,Hkv,N,D]; got q ", q.sizes(), ", K ", K.sizes(), ", V ",
+              V.sizes());
+  const int64_t B = q.size(0), Hq = q.size(1), D = q.size(2), Hkv = K.size(1), N = K.size(2);
+  check_D(D);
+  check_W(W);
+  TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
+  TORCH_CHECK(N >= 1, "N: need at least one cached token");
+  const c10::DeviceGuard guard(q.device());
+  auto o = torch::empty({B, Hq, D}, q.options());
+  auto ws = workspace_for(q, B * Hkv, Hq / Hkv, N, D, FQKV_KV_F16, W);
+  check_rc(fqkv_decode_attn_gqa(q.data_ptr(), K.data_ptr(), V.data_ptr(), o.data_ptr(), B, Hq, Hkv, N, D, W,
+                                ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0,
+                                cur_stream(q)),
+           "launch");
+  return o;
+}
+
+void sk_checks(const torch::Tensor& q, const torch::Tensor& K, const torch::Tensor& V, const torch::Tensor& m_part,
+               const torch::Tensor& l_part, const torch::Tensor& o_part, const torch::Tensor& o, int64_t S,
+               int64_t W, int64_t CW) {
+  check_gpu({&q, &K, &V, &m_part, &l_part, &o_part, &o});
+  check_half(q, "q");
+  check_half(K, "K");
+  check_half(V, "V");
+  check_half(o, "o");
+  TORCH_CHECK(m_part.scalar_type() == torch::kFloat && l_part.scalar_type() == torch::kFloat &&
+                  o_part.scalar_type() == torch::kFloat,
+              "partial: m_part, l_part and o_part must be float32");
+  TORCH_CHECK(q.dim() == 2 && K.dim() == 3 && V.sizes() == K.sizes() && q.size(1) == K.size(2),
+              "shape: expected q [Hq,D], K and V [Hkv,N,D]; got q ", q.sizes(), ", K ", K.sizes(), ", V ",
+              V.sizes());
+  const int64_t Hq = q.size(0), D = q.size(1), Hkv = K.size(0), N = K.size(1);
+  check_D(D);
+  check_W(W);
+  TORCH_CHECK(CW == 4 || CW == 8, "CW: must be 4 or 8, got ", CW);
+  TORCH_CHECK(S >= 1, "S: split count must be >= 1, got ", S);
+  TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
+  TORCH_CHECK(N >= 1, "N: need at least one cached token");
+  TORCH_CHECK(m_part.numel() == Hq * S && l_part.numel() == Hq * S,
+              "partial: m_part and l_part must hold Hq*S = ", Hq * S, " floats");
+  TORCH_CHECK(o_part.numel() == Hq * S * D, "partial: o_part must hold Hq*S*D = ", Hq * S * D, " floats");
+  TORCH_CHECK(o.numel() == Hq * D, "combine: o must hold Hq*D = ", Hq * D, " halves");
+}
+
+// gqa_sk_fast(q[Hq,D], K[Hkv,N,D], V, m_part[Hq,S], l_part[Hq,S], o_part[Hq,S,D], o[Hq,D], S, W, CW)
+void gqa_sk_fast(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor m_part, torch::Tensor l_part,
+                 torch::Tensor o_part, torch::Tensor o, int64_t S, int64_t W, int64_t CW) {
+  sk_checks(q, K, V, m_part, l_part, o_part, o, S, W, CW);
+  const c10::DeviceGuard guard(q.device());
+  check_rc(fqkv_gqa_sk_fast(q.data_ptr(), K.data_ptr(), V.data_ptr(), m_part.data_ptr<float>(),
+                            l_part.data_ptr<float>(), o_part.data_ptr<float>(), o.data_ptr(), q.size(0), K.size(0),
+                            K.size(1), q.size(1), S, W, CW, cur_stream(q)),
+           "launch");
+}
+
+// gqa_sk_fast plus hipEvent records around the partial kernel (timing only).
+void gqa_sk_fast_timed(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor m_part,
+                       torch::Tensor l_part, torch::Tensor o_part, torch::Tensor o, int64_t S, int64_t W,
+                       int64_t CW, int64_t ev_begin, int64_t ev_end) {
+  sk_checks(q, K, V, m_part, l_part, o_part, o, S, W, CW);
+  const c10::DeviceGuard guard(q.device());
+  check_rc(fqkv_gqa_sk_fast_timed(q.data_ptr(), K.data_ptr(), V.data_ptr(), m_part.data_ptr<float>(),
+                                  l_part.data_ptr<float>(), o_part.data_ptr<float>(), o.data_ptr(), q.size(0),
+                                  K.size(0), K.size(1), q.size(1), S, W, CW, cur_stream(q), (void*)ev_begin,
+                                  (void*)ev_end),
+           "launch");
+}
+
+// Dequantise int8 [T,D] / int4 [T,D/2] KV through the kernels' conversions.
+torch::Tensor dequant_kv(torch::Tensor Kq, torch::Tensor Ks, int64_t path) {
+  check_gpu({&Kq, &Ks});
+  check_half(Ks, "Ks");
+  const bool i8 = Kq.scalar_type() == torch::kChar;
+  TORCH_CHECK(i8 || Kq.scalar_type() == torch::kByte, "int8: Kq must be int8 or packed uint8");
+  TORCH_CHECK(Kq.dim() >= 2, "shape: Kq must be [..., D] (int8) or [..., D/2] (int4)");
+  const int64_t D = i8 ? Kq.size(-1) : 2 * Kq.size(-1);
+  check_D(D);
+  const int64_t tokens = Kq.numel() / Kq.size(-1);
+  TORCH_CHECK(Ks.numel() == tokens, "shape: Ks must hold one scale per token row");
+  auto sizes = Kq.sizes().vec();
+  sizes.back() = D;
+  const c10::DeviceGuard guard(Kq.device());
+  auto out = torch::empty(sizes, Kq.options().dtype(torch::kFloat));
+  check_rc(fqkv_dequant_kv(Kq.data_ptr(), Ks.data_ptr(), out.data_ptr<float>(), tokens, D,
+                           i8 ? FQKV_KV_I8 : FQKV_KV_I4, (int)path, cur_stream(Kq)),
+           "launch");
+  return out;
+}
+
+int64_t choose_splits(int64_t rows, int64_t G, int64_t N, int64_t D, int64_t fmt, int64_t W) {
+  return fqkv_choose_splits(rows, G, N, D, (int)fmt, W);
+}
+
+int64_t cu_count() {
+  int c = 0;
+  check_rc(fqkv_device_cu_count(&c), "device");
+  return c;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
+  m.doc() = "MI355X fused single-query decode attention (fp16 / int8-KV / int4-KV / GQA / GQA split-K)";
+  m.def("decode_attn_fp16_mw", &decode_attn_fp16_mw, "fp16 fused decode", py::arg("q"), py::arg("K"), py::arg("V"),
+        py::arg("W"));
+  m.def("decode_attn_int8_mw", &decode_attn_int8_mw, "int8-KV fused decode", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("W"));
+  m.def("decode_attn_int4", &decode_attn_int4, "int4-KV fused decode", py::arg("q"), py::arg("K"), py::arg("V"),
+        py::arg("Ks"), py::arg("Vs"), py::arg("W"));
+  m.def("decode_attn_gqa", &decode_attn_gqa, "GQA-aware fp16 decode", py::arg("q"), py::arg("K"), py::arg("V"),
+        py::arg("W"));
+  m.def("gqa_sk_fast", &gqa_sk_fast, "GQA split-K fp16 decode (partial + combine)", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("m_part"), py::arg("l_part"), py::arg("o_part"), py::arg("o"), py::arg("S"),
+        py::arg("W"), py::arg("CW"));
+  m.def("_gqa_sk_fast_timed", &gqa_sk_fast_timed, "gqa_sk_fast with events around the partial kernel");
+  m.def("_dequant_kv", &dequant_kv, "dequantise int8/int4 KV through the kernels' conversions");
+  m.def("_choose_splits", &choose_splits, "split count the single-block entry points use");
+  m.def("_cu_count", &cu_count, "compute units of the current device");
+  m.def("_version", []() { return std::string(fqkv_version()); });
+}

@@ -1,0 +1,95 @@
+"""MI355X (gfx950) fused single-query decode attention.
+
+Drop-in for the reference's five PyTorch-extension entry points
+(emirabayer/Fused-Quantized-KV-Decode-Attention, kernels/*.cu):
+
+    decode_attn_fp16_mw(q[B,D], K[B,N,D], V, W) -> o[B,D]             (decode_attn_fp16_mw.cu:50)
+    decode_attn_int8_mw(q, K int8, V int8, Ks[B,N], Vs, W) -> o[B,D]  (decode_attn_int8_mw.cu:52)
+    decode_attn_int4(q, K uint8 [B,N,D/2], V, Ks, Vs, W) -> o[B,D]    (decode_attn_int4.cu:47)
+    decode_attn_gqa(q[B,Hq,D], K[B,Hkv,N,D], V, W) -> o[B,Hq,D]       (decode_attn_gqa.cu:56)
+    gqa_sk_fast(q[Hq,D], K[Hkv,N,D], V, m_part, l_part, o_part, o, S, W, CW) -> None
+                                                                      (decode_attn_gqa_sk_fast.cu:95)
+
+Callers of the reference build each kernel with
+``torch.utils.cpp_extension.load(name=..., sources=["kernels/<file>.cu"], ...)``
+and call ``m.<function>(...)``; :func:`load` returns the module that serves
+all five, so ``m = load(name="t_fp16", sources=[...])`` keeps working.
+
+The functions run hand-written HIP kernels from ``libfqkv_decode.so``; there
+is no CPU or PyTorch fallback. Importing this package raises ImportError if
+the native libraries are not built (``python -m fqkv_decode._build``).
+"""
+
+import importlib.util
+import os
+
+import torch  # noqa: F401  (binds the HIP runtime PyTorch ships before ours loads)
+
+from ._build import EXT_NAME, LIB_NAME, PKG_DIR, ext_filename
+
+__all__ = [
+    "decode_attn_fp16_mw",
+    "decode_attn_int8_mw",
+    "decode_attn_int4",
+    "decode_attn_gqa",
+    "gqa_sk_fast",
+    "load",
+    "lib_path",
+    "ext_path",
+]
+
+
+def lib_path():
+    """Path of the C-ABI library libfqkv_decode.so."""
+    return os.path.join(PKG_DIR, LIB_NAME)
+
+
+def ext_path():
+    """Path of the PyTorch binding extension module."""
+    return os.path.join(PKG_DIR, ext_filename())
+
+
+def _load_ext():
+    path = ext_path()
+    if not os.path.exists(path) or not os.path.exists(lib_path()):
+        raise ImportError(
+            "fqkv_decode: native libraries not built (%s); run `python -m fqkv_decode._build` "
+            "from %s" % (path, os.path.dirname(PKG_DIR)))
+    spec = importlib.util.spec_from_file_location("fqkv_decode." + EXT_NAME, path)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+_ext = _load_ext()
+
+decode_attn_fp16_mw = _ext.decode_attn_fp16_mw
+decode_attn_int8_mw = _ext.decode_attn_int8_mw
+decode_attn_int4 = _ext.decode_attn_int4
+decode_attn_gqa = _ext.decode_attn_gqa
+gqa_sk_fast = _ext.gqa_sk_fast
+
+
+def load(name=None, sources=None, extra_cuda_cflags=None, verbose=False, **kwargs):
+    """Stand-in for ``torch.utils.cpp_extension.load`` as the reference's callers use it.
+
+    The reference JIT-compiles one ``.cu`` per entry point
+    (tests/test_kernels.py:8-11,55; flashinfer_looptimed.py:30-31). Here the
+    kernels are prebuilt, so every call returns the one extension module,
+    which exposes all five entry points; the arguments are accepted and
+    ignored.
+    """
+    return _ext
+
+
+def choose_splits(rows, G, N, D, kv_format, W):
+    """Split count the single-block entry points use (1 = none) on the current device.
+
+    ``kv_format`` is 0 (fp16), 1 (int8) or 2 (int4).
+    """
+    return _ext._choose_splits(rows, G, N, D, kv_format, W)
+
+
+def cu_count():
+    """Compute units of the current HIP device."""
+    return _ext._cu_count()

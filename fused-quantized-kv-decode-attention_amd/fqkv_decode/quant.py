@@ -1,0 +1,63 @@
+"""Per-token KV quantizers: the on-memory formats the int8 / int4 kernels read.
+
+PyTorch tensor code, as in the reference, so the bytes match the reference's
+on any device for fp16 and fp32 inputs alike:
+
+* int8: tests/test_kernels.py:32-34 (nb:236-238) -- scale = max|x|/127
+  clamped to >= 1e-8, values round(x/scale) clamped to [-127, 127], scales
+  stored as fp16 [.., N].
+* int4: nb:292-299 -- scale = max|x|/7, values clamped to [-7, 7], packed two
+  per byte with the low nibble holding the even element.
+* dequantisation: nb:301-307 and decode_attn_int8_mw.cu:24,31 --
+  (float)q * (float)scale, exact in fp32.
+"""
+
+import torch
+
+
+def _scales(X, qmax):
+    a = X.abs().amax(-1, keepdim=True)
+    s = (a / float(qmax)).clamp(min=1e-8)
+    return s
+
+
+def quant_int8_per_token(X):
+    """X [..., N, D] (fp16 or fp32) -> (int8 [..., N, D], fp16 scales [..., N])."""
+    s = _scales(X, 127)
+    q = torch.clamp(torch.round(X / s), -127, 127).to(torch.int8).contiguous()
+    return q, s.squeeze(-1).half().contiguous()
+
+
+def pack_int4(q):
+    """int8 values in [-8, 7], [..., D] -> uint8 [..., D/2], low nibble = even element."""
+    q = q.view(*q.shape[:-1], q.shape[-1] // 2, 2)
+    lo = q[..., 0] & 0xF
+    hi = q[..., 1] & 0xF
+    return (lo | (hi << 4)).to(torch.uint8).contiguous()
+
+
+def unpack_int4(packed):
+    """uint8 [..., H] -> int8 [..., 2H]; nibble n >= 8 decodes as n - 16."""
+    b = packed.to(torch.int16)
+    lo = b & 0xF
+    hi = (b >> 4) & 0xF
+    lo = torch.where(lo >= 8, lo - 16, lo)
+    hi = torch.where(hi >= 8, hi - 16, hi)
+    return torch.stack([lo, hi], dim=-1).reshape(*packed.shape[:-1], 2 * packed.shape[-1]).to(torch.int8)
+
+
+def quant_int4_per_token(X):
+    """X [..., N, D] -> (packed uint8 [..., N, D/2], fp16 scales [..., N])."""
+    s = _scales(X, 7)
+    q = torch.clamp(torch.round(X / s), -7, 7).to(torch.int8)
+    return pack_int4(q), s.squeeze(-1).half().contiguous()
+
+
+def dequant_int8(q, s):
+    """(float)q * (float)scale -> fp32 [..., N, D]."""
+    return q.float() * s.float()[..., None]
+
+
+def dequant_int4(packed, s):
+    """Unpack (low nibble first), then (float)q * (float)scale -> fp32 [..., N, D]."""
+    return unpack_int4(packed).float() * s.float()[..., None]

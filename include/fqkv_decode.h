@@ -1,0 +1,152 @@
+/*
+ * fqkv_decode.h -- C ABI of the MI355X (gfx950) fused single-query
+ * decode-attention library (libfqkv_decode.so).
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer to
+ * contiguous memory, every size is a 64-bit integer, `stream` is a
+ * hipStream_t passed as void* (NULL = the legacy default stream). All calls
+ * are asynchronous on `stream`; none synchronises the device and none
+ * allocates device memory (callers pass any workspace).
+ *
+ * Data formats (the reference's layouts, unchanged):
+ *   fp16 KV        K, V: [rows, N, D] __half, row-major
+ *   int8 KV        K, V: [rows, N, D] int8, per-token scales Ks, Vs: [rows, N] __half
+ *   int4 KV        K, V: [rows, N, D/2] uint8, two values per byte, low nibble
+ *                  = even element (byte t holds elements 2t, 2t+1); a nibble n
+ *                  decodes as n - 16 when n >= 8; scales as for int8
+ *   dequantised value = (float)q * (float)scale, exact in fp32
+ *   softmax scale  = 1.0f / sqrtf((float)D); D (head_dim) is 64 or 128
+ *
+ * Return value: FQKV_OK (0) on success; otherwise a non-zero FQKV_ERR_* code
+ * and fqkv_last_error() describes the failure (thread-local). Argument
+ * checks run before any HIP call.
+ *
+ * Reference interfaces are cited as file:line of
+ * emirabayer/Fused-Quantized-KV-Decode-Attention.
+ */
+#ifndef FQKV_DECODE_H
+#define FQKV_DECODE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  FQKV_OK = 0,
+  FQKV_ERR_ARG = 1, /* invalid argument (shape, tuning knob, null pointer, workspace) */
+  FQKV_ERR_HIP = 2  /* a HIP runtime call or kernel launch failed */
+};
+
+enum { FQKV_KV_F16 = 0, FQKV_KV_I8 = 1, FQKV_KV_I4 = 2 };
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* fqkv_last_error(void);
+
+/* Library version string. */
+const char* fqkv_version(void);
+
+/*
+ * Workspace (bytes) the single-block entry points below use to split a long
+ * sequence across workgroups when `rows` alone cannot fill the GPU:
+ * rows = batch*kv_heads, G = query heads per KV head (1 for MHA), kv_format
+ * FQKV_KV_*, W the waves-per-workgroup knob. Returns 0 when no split is used.
+ * A smaller (or NULL) workspace is legal: the entry point then uses as many
+ * splits as fit, down to none. Queries the current device's CU count.
+ */
+size_t fqkv_workspace_bytes(int64_t rows, int64_t G, int64_t N, int64_t D, int kv_format,
+                            int64_t W);
+
+/*
+ * fp16 MHA decode: o[b] = fp16(softmax(q[b] . K[b]^T / sqrt(D)) V[b]).
+ * q: [B, D] fp16, K, V: [B, N, D] fp16, o: [B, D] fp16. W in {2, 4, 8}.
+ * Replaces decode_attn_fp16_mw(q, K, V, W) (kernels/decode_attn_fp16_mw.cu:50-63).
+ */
+int fqkv_decode_attn_fp16_mw(const void* q, const void* K, const void* V, void* o, int64_t B,
+                             int64_t N, int64_t D, int64_t W, void* workspace,
+                             size_t workspace_bytes, void* stream);
+
+/*
+ * int8-KV MHA decode with per-token fp16 scales.
+ * q: [B, D] fp16, K, V: [B, N, D] int8, Ks, Vs: [B, N] fp16, o: [B, D] fp16.
+ * Replaces decode_attn_int8_mw(q, K, V, Ks, Vs, W) (kernels/decode_attn_int8_mw.cu:52-64).
+ */
+int fqkv_decode_attn_int8_mw(const void* q, const void* K, const void* V, const void* Ks,
+                             const void* Vs, void* o, int64_t B, int64_t N, int64_t D,
+                             int64_t W, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * int4-KV MHA decode (packed, low nibble first) with per-token fp16 scales.
+ * q: [B, D] fp16, K, V: [B, N, D/2] uint8, Ks, Vs: [B, N] fp16, o: [B, D] fp16.
+ * D is the unpacked head_dim (64 or 128; the reference supports 64 only).
+ * Replaces decode_attn_int4(q, K, V, Ks, Vs, W) (kernels/decode_attn_int4.cu:47-57).
+ */
+int fqkv_decode_attn_int4(const void* q, const void* K, const void* V, const void* Ks,
+                          const void* Vs, void* o, int64_t B, int64_t N, int64_t D, int64_t W,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * GQA-aware fp16 decode: query head h of batch b reads KV head h / (Hq/Hkv).
+ * q: [B, Hq, D], K, V: [B, Hkv, N, D], o: [B, Hq, D], all fp16; Hq % Hkv == 0.
+ * Replaces decode_attn_gqa(q, K, V, W) (kernels/decode_attn_gqa.cu:56-68).
+ */
+int fqkv_decode_attn_gqa(const void* q, const void* K, const void* V, void* o, int64_t B,
+                         int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int64_t W,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * GQA split-K fp16 decode (partial kernel + combine kernel).
+ * q: [Hq, D] fp16, K, V: [Hkv, N, D] fp16, caller-owned fp32 scratch
+ * m_part, l_part: [Hq, S], o_part: [Hq, S, D], output o: [Hq, D] fp16.
+ * Split s covers tokens [s*c, min(s*c + c, N)) with c = ceil(N/S). Every
+ * scratch entry is written: m_part = max score (natural-log units, i.e.
+ * scaled by 1/sqrt(D)), l_part = sum exp(score - m), o_part = unnormalised
+ * sum exp(score - m) V; an empty split stores (-inf, 0, 0).
+ * A batch folds into the head axis: q [B*Hq, D], K [B*Hkv, N, D].
+ * W in {2, 4, 8} waves per partial workgroup, CW in {4, 8} combine waves.
+ * Replaces gqa_sk_fast(q, K, V, m_part, l_part, o_part, o, S, W, CW)
+ * (kernels/decode_attn_gqa_sk_fast.cu:95-112).
+ */
+int fqkv_gqa_sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l_part,
+                     float* o_part, void* o, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
+                     int64_t S, int64_t W, int64_t CW, void* stream);
+
+/*
+ * Same as fqkv_gqa_sk_fast, additionally recording the hipEvent_t handles
+ * ev_begin / ev_end on `stream` immediately before and after the partial
+ * kernel, so a caller can time that kernel alone. Either event may be NULL.
+ * Instrumented form of decode_attn_gqa_sk_fast.cu:95-112 (no counterpart call).
+ */
+int fqkv_gqa_sk_fast_timed(const void* q, const void* K, const void* V, float* m_part,
+                           float* l_part, float* o_part, void* o, int64_t Hq, int64_t Hkv,
+                           int64_t N, int64_t D, int64_t S, int64_t W, int64_t CW, void* stream,
+                           void* ev_begin, void* ev_end);
+
+/*
+ * Dequantise an int8 or int4 KV tensor with the exact device conversion the
+ * attention kernels use, writing out[t, d] = (float)q[t, d] * (float)scale[t]
+ * for tokens = rows*N token rows. path 0 = the K-side conversion (int -> fp16
+ * matrix-core operand), path 1 = the V-side conversion (int -> fp32).
+ * Format check for tests/golden bit-exactness; mirrors the kernels' dequant at
+ * decode_attn_int8_mw.cu:24,31 and decode_attn_int4.cu:21-23,29-31.
+ */
+int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, int64_t D,
+                    int kv_format, int path, void* stream);
+
+/* Number of compute units of the current device (used by the split heuristic). */
+int fqkv_device_cu_count(int* cu_count);
+
+/*
+ * Splits the single-block entry points use for a problem (1 = no split), as
+ * chosen from the current device's CU count; exposed for tests and tooling.
+ */
+int64_t fqkv_choose_splits(int64_t rows, int64_t G, int64_t N, int64_t D, int kv_format,
+                           int64_t W);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FQKV_DECODE_H */

@@ -1,0 +1,130 @@
+"""The drop-in boundary without a GPU: the C-ABI library loads, exports every
+symbol include/fqkv_decode.h declares, and rejects bad arguments before any
+HIP call; the PyTorch binding exposes the reference's five names and refuses
+CPU tensors with the reference's "cuda" error."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+import fqkv_decode
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fqkv_decode.h")
+
+I64 = ctypes.c_int64
+VP = ctypes.c_void_p
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fqkv_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    L = ctypes.CDLL(fqkv_decode.lib_path())
+    L.fqkv_last_error.restype = ctypes.c_char_p
+    L.fqkv_version.restype = ctypes.c_char_p
+    return L
+
+
+def test_header_declares_the_five_entry_points():
+    syms = declared_symbols()
+    for name in ("fqkv_decode_attn_fp16_mw", "fqkv_decode_attn_int8_mw", "fqkv_decode_attn_int4",
+                 "fqkv_decode_attn_gqa", "fqkv_gqa_sk_fast"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol(lib):
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_library_has_no_torch_dependency():
+    import subprocess
+
+    out = subprocess.run(["readelf", "-d", fqkv_decode.lib_path()], capture_output=True, text=True).stdout
+    needed = re.findall(r"NEEDED.*\[(.*)\]", out)
+    assert not any("torch" in n or "c10" in n for n in needed), needed
+    assert any(n.startswith("libamdhip64") for n in needed)
+
+
+def test_version(lib):
+    assert b"gfx950" in lib.fqkv_version()
+
+
+def _err(lib):
+    return lib.fqkv_last_error().decode()
+
+
+@pytest.mark.parametrize("B,N,D,W,key", [
+    (1, 16, 96, 8, "D:"), (1, 16, 64, 3, "W:"), (1, 0, 64, 8, "N:"), (0, 16, 64, 8, "B:"),
+])
+def test_capi_fp16_rejects_bad_shapes(lib, B, N, D, W, key):
+    f = lib.fqkv_decode_attn_fp16_mw
+    f.argtypes = [VP, VP, VP, VP, I64, I64, I64, I64, VP, ctypes.c_size_t, VP]
+    rc = f(16, 16, 16, 16, B, N, D, W, None, 0, None)
+    assert rc == 1 and _err(lib).startswith(key), _err(lib)
+
+
+def test_capi_rejects_null_and_misaligned_pointers(lib):
+    f = lib.fqkv_decode_attn_fp16_mw
+    f.argtypes = [VP, VP, VP, VP, I64, I64, I64, I64, VP, ctypes.c_size_t, VP]
+    assert f(None, 16, 16, 16, 1, 16, 64, 8, None, 0, None) == 1 and "null" in _err(lib)
+    assert f(16, 24, 16, 16, 1, 16, 64, 8, None, 0, None) == 1 and "aligned" in _err(lib)
+
+
+def test_capi_sk_fast_rejects_bad_knobs(lib):
+    f = lib.fqkv_gqa_sk_fast
+    f.argtypes = [VP, VP, VP, VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, I64, VP]
+    args = [16] * 7
+    assert f(*args, 32, 8, 1024, 128, 16, 8, 5, None) == 1 and _err(lib).startswith("CW:")
+    assert f(*args, 32, 8, 1024, 128, 0, 8, 4, None) == 1 and _err(lib).startswith("S:")
+    assert f(*args, 30, 8, 1024, 128, 16, 8, 4, None) == 1 and _err(lib).startswith("heads:")
+    assert f(*args, 32, 8, 1024, 128, 16, 6, 4, None) == 1 and _err(lib).startswith("W:")
+    assert f(*args, 32, 8, 1024, 100, 16, 8, 4, None) == 1 and _err(lib).startswith("D:")
+
+
+def test_capi_quant_and_gqa_reject_bad_args(lib):
+    f8 = lib.fqkv_decode_attn_int8_mw
+    f8.argtypes = [VP, VP, VP, VP, VP, VP, I64, I64, I64, I64, VP, ctypes.c_size_t, VP]
+    assert f8(16, 16, 16, None, 16, 16, 2, 64, 128, 8, None, 0, None) == 1 and "null" in _err(lib)
+    f4 = lib.fqkv_decode_attn_int4
+    f4.argtypes = f8.argtypes
+    assert f4(16, 16, 16, 16, 16, 16, 2, 64, 32, 8, None, 0, None) == 1 and _err(lib).startswith("D:")
+    fg = lib.fqkv_decode_attn_gqa
+    fg.argtypes = [VP, VP, VP, VP, I64, I64, I64, I64, I64, I64, VP, ctypes.c_size_t, VP]
+    assert fg(16, 16, 16, 16, 1, 32, 6, 64, 64, 8, None, 0, None) == 1 and _err(lib).startswith("heads:")
+    fd = lib.fqkv_dequant_kv
+    fd.argtypes = [VP, VP, VP, I64, I64, ctypes.c_int, ctypes.c_int, VP]
+    assert fd(16, 16, 16, 4, 128, 0, 0, None) == 1 and "kv_format" in _err(lib)
+
+
+def test_binding_exposes_reference_names():
+    m = fqkv_decode.load(name="t_fp16", sources=["kernels/decode_attn_fp16_mw.cu"], extra_cuda_cflags=["-O3"])
+    for name in ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa", "gqa_sk_fast"):
+        assert callable(getattr(m, name))
+        assert getattr(fqkv_decode, name) is getattr(m, name)
+
+
+def test_binding_rejects_cpu_tensors():
+    q = torch.zeros(1, 64, dtype=torch.float16)
+    K = torch.zeros(1, 8, 64, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="^cuda"):
+        fqkv_decode.decode_attn_fp16_mw(q, K, K, 8)
+    with pytest.raises(RuntimeError, match="^cuda"):
+        fqkv_decode.decode_attn_gqa(q.view(1, 1, 64), K.view(1, 1, 8, 64), K.view(1, 1, 8, 64), 8)
+    Kq = torch.zeros(1, 8, 64, dtype=torch.int8)
+    s = torch.zeros(1, 8, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="^cuda"):
+        fqkv_decode.decode_attn_int8_mw(q, Kq, Kq, s, s, 8)
+    with pytest.raises(RuntimeError, match="^cuda"):
+        fqkv_decode.decode_attn_int4(q, Kq.view(torch.uint8)[..., :32].contiguous(), Kq.view(torch.uint8)[..., :32].contiguous(), s, s, 8)
+    mp = torch.zeros(1, 4)
+    with pytest.raises(RuntimeError, match="^cuda"):
+        fqkv_decode.gqa_sk_fast(q, K, K, mp, mp, torch.zeros(1, 4, 64), q.clone(), 4, 8, 4)
