@@ -203,6 +203,8 @@ def main():
     ap.add_argument("--kv-sets", type=int, default=10, help="distinct 64 MiB KV caches cycled through")
     ap.add_argument("--sweep", action="store_true", help="tune S/W/CW first (table on stderr)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="first run a plain device copy of this many MiB (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -215,6 +217,15 @@ def main():
     import fqkv_decode as fq
 
     cus = fq.cu_count()
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("calibration copy: 3 x %d MiB device-to-device" % args.calib_copy_mib)
+        del src, dst
     q, Ks, Vs = make_sets(torch, args.kv_sets)
     S, W, CW = (args.S or default_splits(cus)), args.W, args.CW
 

@@ -142,7 +142,16 @@ int run_decode(int fmt, const void* q, const void* K, const void* V, const void*
 int check_ptrs_kv(const void* q, const void* K, const void* V, const void* o) {
   if (!q || !K || !V || !o) return fail(FQKV_ERR_ARG, "null tensor pointer");
   if (!aligned(K, 16) || !aligned(V, 16)) return fail(FQKV_ERR_ARG, "K and V must be 16-byte aligned");
-  if (!aligned(q, 2) || !aligned(o, 2)) return fail(FQKV_ERR_ARG, "q and o must be 2-byte aligned");
+  if (!aligned(q, 16) || !aligned(o, 2)) return fail(FQKV_ERR_ARG, "q must be 16-byte and o 2-byte aligned");
+  return FQKV_OK;
+}
+
+// The kernels address a KV row block with 32-bit byte offsets.
+int check_span(int64_t N, int64_t D, int fmt) {
+  const int64_t row_bytes = fmt == KV_F16 ? 2 * D : (fmt == KV_I8 ? D : D / 2);
+  if (N * row_bytes > (int64_t)UINT32_MAX)
+    return fail(FQKV_ERR_ARG, "N: %lld tokens of %lld bytes exceed the 4 GiB per-row span", (long long)N,
+                (long long)row_bytes);
   return FQKV_OK;
 }
 
@@ -157,6 +166,7 @@ int sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l
     return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
   rc = check_ptrs_kv(q, K, V, o);
   if (rc) return rc;
+  if ((rc = check_span(N, D, KV_F16))) return rc;
   if (!m_part || !l_part || !o_part) return fail(FQKV_ERR_ARG, "null scratch pointer");
   if (!aligned(o_part, 8)) return fail(FQKV_ERR_ARG, "o_part must be 8-byte aligned");
   const int64_t G = Hq / Hkv;
@@ -224,6 +234,7 @@ int fqkv_decode_attn_fp16_mw(const void* q, const void* K, const void* V, void* 
   if (rc) return rc;
   if (B < 1) return fail(FQKV_ERR_ARG, "B: batch must be >= 1, got %lld", (long long)B);
   if ((rc = check_ptrs_kv(q, K, V, o))) return rc;
+  if ((rc = check_span(N, D, KV_F16))) return rc;
   return run_decode(KV_F16, q, K, V, nullptr, nullptr, o, B, 1, N, D, W, workspace, workspace_bytes,
                     (hipStream_t)stream);
 }
@@ -237,8 +248,9 @@ static int quant_entry(int fmt, const void* q, const void* K, const void* V, con
   if (!q || !K || !V || !Ks || !Vs || !o) return fail(FQKV_ERR_ARG, "null tensor pointer");
   const uintptr_t kal = (fmt == KV_I4 && D == 64) ? 8 : 16;
   if (!aligned(K, kal) || !aligned(V, kal)) return fail(FQKV_ERR_ARG, "K and V must be %d-byte aligned", (int)kal);
-  if (!aligned(q, 2) || !aligned(o, 2) || !aligned(Ks, 2) || !aligned(Vs, 2))
-    return fail(FQKV_ERR_ARG, "q, o and scales must be 2-byte aligned");
+  if (!aligned(q, 16) || !aligned(o, 2) || !aligned(Ks, 2) || !aligned(Vs, 2))
+    return fail(FQKV_ERR_ARG, "q must be 16-byte aligned, o and scales 2-byte aligned");
+  if ((rc = check_span(N, D, fmt))) return rc;
   return run_decode(fmt, q, K, V, Ks, Vs, o, B, 1, N, D, W, workspace, workspace_bytes,
                     (hipStream_t)stream);
 }
@@ -264,6 +276,7 @@ int fqkv_decode_attn_gqa(const void* q, const void* K, const void* V, void* o, i
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
     return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
   if ((rc = check_ptrs_kv(q, K, V, o))) return rc;
+  if ((rc = check_span(N, D, KV_F16))) return rc;
   return run_decode(KV_F16, q, K, V, nullptr, nullptr, o, B * Hkv, Hq / Hkv, N, D, W, workspace,
                     workspace_bytes, (hipStream_t)stream);
 }

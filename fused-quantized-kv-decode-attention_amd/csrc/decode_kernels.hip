@@ -4,9 +4,13 @@
 // (KV row r, query-head group, split s) work item: it streams the split's
 // K/V token range of KV row r exactly once and applies it to up to HG query
 // heads of that row (HG = 1 for MHA; the GQA group for GQA), so compact GQA
-// KV is read once per group instead of once per query head. Per 16-token
-// tile a wave
-//   1. loads the K tile as matrix-core operand B (dwordx4, 64 contiguous
+// KV is read once per group instead of once per query head. Waves take
+// interleaved 16-token tiles in passes of U tiles: a pass first issues every
+// load of its U tiles (raw buffer loads from a descriptor that ends at the
+// split's last token, so rows past it read as zeros and need no clamping),
+// then consumes the tiles in order while the later ones are still arriving.
+// Per tile a wave
+//   1. has loaded the K tile as matrix-core operand B (dwordx4, 64 contiguous
 //      bytes per row per instruction) and the V tile as 16-byte row slices,
 //   2. computes all HG x 16 scores with D/32 v_mfma_f32_16x16x32_f16 (query
 //      head slots on the M axis, tokens on N),
@@ -65,6 +69,7 @@ __device__ __forceinline__ void compiler_fence() { __asm__ __volatile__("" ::: "
 template <int FMT, int D, int HG>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
+  constexpr int U = 4;
   constexpr int NR = (HG + 3) / 4;  // MFMA result registers that carry heads
   __shared__ float s_w[NW_MAX][16][HG];
   __shared__ float s_o[NW_MAX][HG][D];
@@ -72,7 +77,8 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   __shared__ float s_l[NW_MAX][HG];
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  // wave index as a scalar, so tile loops branch per wave, not per lane
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
   int wg = blockIdx.x;
   const int s = wg % p.S;
@@ -96,16 +102,15 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 
   // Query fragment (MFMA operand A). Row m = lane % 16 carries head slot
   // 4 (m % 4) + m / 4, so result register rr of lane l holds head (l / 16) + 4 rr.
+  // The descriptor covers only this group's hcnt query rows: slots past them
+  // read as zeros and score nothing.
   h8_t qa[F::NKI];
   {
     const int m = lane & 15;
     const int h = 4 * (m & 3) + (m >> 2);
-    const bool hv = h < hcnt;
-    const _Float16* qh = p.q + (qrow0 + (hv ? h : 0)) * D;
+    const rsrc_t rQ = make_rsrc(p.q + qrow0 * D, (uint32_t)hcnt * D * 2);
 #pragma unroll
-    for (int i = 0; i < F::NKI; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qa[i][e] = hv ? qh[F::kd_index(i, kb, e)] : (_Float16)0.0f;
+    for (int i = 0; i < F::NKI; ++i) qa[i] = F::qfrag(rQ, (uint32_t)h * D, i, kb);
   }
 
   float m_run[NR], l_run[NR], c_run[NR];
@@ -121,46 +126,57 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
     for (int e = 0; e < F::EV; ++e) acc[h][e] = 0.0f;
 
-  for (int tb = lo + 16 * w; tb < hi; tb += 16 * nw) {
-    const int tk = tb + kt;
-    const int tkc = min(tk, hi - 1);  // clamp: masked tokens re-read a valid row
-    uint32_t kd[F::KDW];
-    F::load_k(Kr + (size_t)tkc * F::ROWB, kb, kd);
-    float ksc = 1.0f, vsc = 1.0f;
+  struct Tile {
+    typename F::KT kr[F::KL];
+    vraw_t<F::VB> vr[F::VLD];
+    float ksc, vsc;
+  };
+  // Buffer descriptors end at the split's last token, so rows past it read
+  // as zeros (their scores are masked); offsets are 32-bit from the row block.
+  const uint32_t nbytes = (uint32_t)hi * F::ROWB;
+  const rsrc_t rK = make_rsrc(Kr, nbytes);
+  const rsrc_t rV = make_rsrc(Vr, nbytes);
+  const rsrc_t rKs = make_rsrc(Ksr, 2u * (uint32_t)hi);
+  const rsrc_t rVs = make_rsrc(Vsr, 2u * (uint32_t)hi);
+  const uint32_t koff = (uint32_t)kt * F::ROWB + F::klane(kb);
+  const uint32_t voff = (uint32_t)vt * F::ROWB + (uint32_t)vl * F::VB;
+  auto load_tile = [&](Tile& t, int tb) {
+    const uint32_t base = (uint32_t)tb * F::ROWB;
+    F::load_k(rK, base + koff, t.kr);
     if constexpr (F::QUANT) {
-      ksc = (float)Ksr[tkc];
-      vsc = (float)Vsr[tkc];
+      t.ksc = (float)__builtin_bit_cast(_Float16, buf_load<2>(rKs, 2u * (uint32_t)(tb + kt)));
+      t.vsc = (float)__builtin_bit_cast(_Float16, buf_load<2>(rVs, 2u * (uint32_t)(tb + kt)));
+    } else {
+      t.ksc = 1.0f;
+      t.vsc = 1.0f;
     }
-    uint32_t vd[F::VLD][F::VB / 4];
 #pragma unroll
-    for (int j = 0; j < F::VLD; ++j) {
-      const int tv = min(tb + j * F::TPL + vt, hi - 1);
-      load_v<FMT, D>(Vr + (size_t)tv * F::ROWB, vl, vd[j]);
-    }
-
+    for (int j = 0; j < F::VLD; ++j) t.vr[j] = load_v<FMT, D>(rV, base + voff + (uint32_t)(j * F::TPL * F::ROWB));
+  };
+  // Scores, online-softmax step and p*V accumulation for one loaded tile.
+  auto process_tile = [&](const Tile& t, int tb) {
     f4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int i = 0; i < F::NKI; ++i)
-      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[i], F::kfrag(kd, i), c4, 0, 0, 0);
-
+      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[i], F::kfrag(t.kr, i), c4, 0, 0, 0);
+    const bool tok_ok = tb + kt < hi;
     float alpha[NR];
 #pragma unroll
     for (int rr = 0; rr < NR; ++rr) {
       const int h = kb + 4 * rr;
-      float x = c4[rr] * ksc;
-      x = (tk < hi && h < hcnt) ? x : -INFINITY;
+      float x = c4[rr] * t.ksc;
+      x = (tok_ok && h < hcnt) ? x : -INFINITY;
       const float mn = fmaxf(m_run[rr], row16_max(x));
       const float mu = (mn == -INFINITY) ? 0.0f : mn;
       alpha[rr] = fast_exp2((m_run[rr] - mu) * p.c);
       const float pw = fast_exp2((x - mu) * p.c);
       l_run[rr] = l_run[rr] * alpha[rr] + pw;
-      const float wv = pw * vsc;
+      const float wv = pw * t.vsc;
       if constexpr (F::QUANT) c_run[rr] = c_run[rr] * alpha[rr] + wv;
       m_run[rr] = mn;
       if (h < HG) s_w[w][kt][h] = wv;
     }
     compiler_fence();
-
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
       const float a = readlane_f(alpha[h / 4], 16 * (h % 4));
@@ -176,13 +192,31 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
       for (int h = 0; h < HG; ++h) wt[h] = s_w[w][tl][h];
       float f[F::EV];
-      F::vconv(vd[j], f);
+      F::vconv(t.vr[j], f);
 #pragma unroll
       for (int h = 0; h < HG; ++h)
 #pragma unroll
         for (int e = 0; e < F::EV; ++e) acc[h][e] = fmaf(wt[h], f[e], acc[h][e]);
     }
     compiler_fence();
+  };
+
+  // Two-tile register pipeline: the next tile's loads are in flight while the
+  // current tile is processed. Every branch below is wave-uniform, and each
+  // path either prefetches before processing or processes the last tile, so
+  // the compiler's load counters wait only for the tile being consumed.
+  // Each pass a wave issues the loads of U tiles (interleaved with the other
+  // waves' tiles) before consuming any: straight-line code, so the load
+  // counter waits exactly for the tile about to be used while the rest of the
+  // pass is still in flight. Tiles past the split end are clamped and masked.
+  const int step = 16 * nw;
+  for (int pb = lo + 16 * w; pb < hi; pb += U * step) {
+    Tile t[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) load_tile(t[u], pb + u * step);
+    __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
+#pragma unroll
+    for (int u = 0; u < U; ++u) process_tile(t[u], pb + u * step);
   }
 
   // ---- wave totals ----
@@ -323,12 +357,12 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
     const int64_t t = g / 4;
     const int kb = (int)(g % 4);
     if (t >= tokens) return;
-    uint32_t kd[F::KDW];
-    F::load_k(Kq + t * F::ROWB, kb, kd);
+    typename F::KT kr[F::KL];
+    F::load_k(make_rsrc(Kq + t * F::ROWB, F::ROWB), F::klane(kb), kr);
     const float sc = (float)Ks[t];
 #pragma unroll
     for (int i = 0; i < F::NKI; ++i) {
-      const h8_t b = F::kfrag(kd, i);
+      const h8_t b = F::kfrag(kr, i);
 #pragma unroll
       for (int e = 0; e < 8; ++e) out[t * D + F::kd_index(i, kb, e)] = (float)b[e] * sc;
     }
@@ -336,10 +370,8 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
     const int64_t t = g / F::LPR;
     const int lir = (int)(g % F::LPR);
     if (t >= tokens) return;
-    uint32_t vd[F::VB / 4];
-    load_v<FMT, D>(Kq + t * F::ROWB, lir, vd);
     float f[F::EV];
-    F::vconv(vd, f);
+    F::vconv(load_v<FMT, D>(make_rsrc(Kq + t * F::ROWB, F::ROWB), (uint32_t)lir * F::VB), f);
     const float sc = (float)Ks[t];
 #pragma unroll
     for (int e = 0; e < F::EV; ++e) out[t * D + F::vd_index(lir, e)] = (f[e] - F::VBIAS) * sc;

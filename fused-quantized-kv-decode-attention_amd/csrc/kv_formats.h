@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace fqkv {
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
@@ -66,6 +68,23 @@ __device__ __forceinline__ float ubyte_f(uint32_t w, int k) {
   return (float)((w >> (8 * k)) & 0xFFu);  // v_cvt_f32_ubyte{k}
 }
 
+// Raw buffer access (gfx9 descriptor word 3 = 0x00020000, stride 0):
+// loads whose byte offset is at or past num_records return zeros.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+template <int BYTES>
+__device__ __forceinline__ auto buf_load(rsrc_t r, uint32_t off) {
+  if constexpr (BYTES == 16) {
+    return __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+  } else if constexpr (BYTES == 8) {
+    return __builtin_bit_cast(u2_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+  } else {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+  }
+}
+
 template <int FMT, int D>
 struct Fmt;
 
@@ -75,22 +94,22 @@ struct Fmt<KV_F16, D> {
   static constexpr bool QUANT = false;
   static constexpr int ROWB = 2 * D;  // bytes per token row
   static constexpr int NKI = D / 32;  // MFMA steps per tile
-  static constexpr int KDW = D / 8;   // K dwords per lane per tile
+  using KT = u4_t;                    // one K load
+  static constexpr int KL = D / 32;   // K loads per lane per tile
   // Step i, lane group kb reads row bytes [64 i + 16 kb, +16): each load
   // instruction covers 64 contiguous bytes of 16 rows.
-  __device__ static void load_k(const uint8_t* row, int kb, uint32_t (&kd)[KDW]) {
+  __host__ __device__ static constexpr uint32_t klane(int kb) { return 16 * kb; }
+  __device__ static void load_k(rsrc_t r, uint32_t off, KT (&kr)[KL]) {
 #pragma unroll
-    for (int j = 0; j < NKI; ++j) {
-      const u4_t v = *reinterpret_cast<const u4_t*>(row + 64 * j + 16 * kb);
-      kd[4 * j + 0] = v.x; kd[4 * j + 1] = v.y; kd[4 * j + 2] = v.z; kd[4 * j + 3] = v.w;
-    }
+    for (int j = 0; j < KL; ++j) kr[j] = buf_load<16>(r, off + 64 * j);
   }
-  __device__ static h8_t kfrag(const uint32_t (&kd)[KDW], int i) {
-    u4_t v = {kd[4 * i], kd[4 * i + 1], kd[4 * i + 2], kd[4 * i + 3]};
-    return __builtin_bit_cast(h8_t, v);
-  }
+  __device__ static h8_t kfrag(const KT (&kr)[KL], int i) { return __builtin_bit_cast(h8_t, kr[i]); }
   __host__ __device__ static constexpr int kd_index(int i, int kb, int e) {
     return 32 * i + 8 * kb + e;
+  }
+  // Query operand for step i: the same eight head-dim elements as kfrag.
+  __device__ static h8_t qfrag(rsrc_t rq, uint32_t row_elem, int i, int kb) {
+    return __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
   }
   static constexpr int VB = 16;              // bytes per lane per V load
   static constexpr int LPR = ROWB / VB;      // lanes per token row
@@ -98,10 +117,13 @@ struct Fmt<KV_F16, D> {
   static constexpr int VLD = 16 / TPL;       // V loads per tile
   static constexpr int EV = 8;               // elements per lane per V load
   static constexpr float VBIAS = 0.0f;
-  __device__ static void vconv(const uint32_t (&vd)[VB / 4], float (&f)[EV]) {
+  __device__ static void vconv(const u4_t vd, float (&f)[EV]) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const h2_t h = __builtin_bit_cast(h2_t, vd[k]);
+      // element copied to a scalar first: this compiler's __builtin_bit_cast of
+      // a vector-element expression reads element 0 whatever the index
+      const uint32_t x = vd[k];
+      const h2_t h = __builtin_bit_cast(h2_t, x);
       f[2 * k] = (float)h.x;
       f[2 * k + 1] = (float)h.y;
     }
@@ -115,23 +137,26 @@ struct Fmt<KV_I8, D> {
   static constexpr bool QUANT = true;
   static constexpr int ROWB = D;
   static constexpr int NKI = D / 32;
-  static constexpr int KDW = D / 16;
+  using KT = u4_t;
+  static constexpr int KL = D / 64;
   // Load j, lane group kb reads row bytes [64 j + 16 kb, +16) = two MFMA steps.
-  __device__ static void load_k(const uint8_t* row, int kb, uint32_t (&kd)[KDW]) {
+  __host__ __device__ static constexpr uint32_t klane(int kb) { return 16 * kb; }
+  __device__ static void load_k(rsrc_t r, uint32_t off, KT (&kr)[KL]) {
 #pragma unroll
-    for (int j = 0; j < D / 64; ++j) {
-      const u4_t v = *reinterpret_cast<const u4_t*>(row + 64 * j + 16 * kb);
-      kd[4 * j + 0] = v.x; kd[4 * j + 1] = v.y; kd[4 * j + 2] = v.z; kd[4 * j + 3] = v.w;
-    }
+    for (int j = 0; j < KL; ++j) kr[j] = buf_load<16>(r, off + 64 * j);
   }
-  __device__ static h8_t kfrag(const uint32_t (&kd)[KDW], int i) {
+  __device__ static h8_t kfrag(const KT (&kr)[KL], int i) {
+    const u4_t v = kr[i / 2];
     h2_t a, b, c, d;
-    i8x4_to_h2x2(kd[2 * i], a, b);
-    i8x4_to_h2x2(kd[2 * i + 1], c, d);
+    i8x4_to_h2x2((i % 2) ? v.z : v.x, a, b);
+    i8x4_to_h2x2((i % 2) ? v.w : v.y, c, d);
     return h8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
   }
   __host__ __device__ static constexpr int kd_index(int i, int kb, int e) {
     return 64 * (i / 2) + 16 * kb + 8 * (i % 2) + e;
+  }
+  __device__ static h8_t qfrag(rsrc_t rq, uint32_t row_elem, int i, int kb) {
+    return __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
   }
   static constexpr int VB = 16;
   static constexpr int LPR = ROWB / VB;
@@ -139,7 +164,7 @@ struct Fmt<KV_I8, D> {
   static constexpr int VLD = 16 / TPL;
   static constexpr int EV = 16;
   static constexpr float VBIAS = 128.0f;  // vconv yields x + 128
-  __device__ static void vconv(const uint32_t (&vd)[VB / 4], float (&f)[EV]) {
+  __device__ static void vconv(const u4_t vd, float (&f)[EV]) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint32_t t = vd[k] ^ 0x80808080u;
@@ -156,25 +181,26 @@ struct Fmt<KV_I4, D> {
   static constexpr bool QUANT = true;
   static constexpr int ROWB = D / 2;
   static constexpr int NKI = D / 32;
-  static constexpr int KDW = D / 32;  // one dword (8 elements) per MFMA step
+  // one load of ROWB/4 bytes (one dword = 8 elements per MFMA step)
+  using KT = typename std::conditional<D == 128, u4_t, u2_t>::type;
+  static constexpr int KL = 1;
   // Lane group kb reads row bytes [ROWB/4 * kb, +ROWB/4): four lanes cover a row.
-  __device__ static void load_k(const uint8_t* row, int kb, uint32_t (&kd)[KDW]) {
-    if constexpr (D == 128) {
-      const u4_t v = *reinterpret_cast<const u4_t*>(row + 16 * kb);
-      kd[0] = v.x; kd[1] = v.y; kd[2] = v.z; kd[3] = v.w;
-    } else {
-      const u2_t v = *reinterpret_cast<const u2_t*>(row + 8 * kb);
-      kd[0] = v.x; kd[1] = v.y;
-    }
+  __host__ __device__ static constexpr uint32_t klane(int kb) { return (ROWB / 4) * kb; }
+  __device__ static void load_k(rsrc_t r, uint32_t off, KT (&kr)[KL]) {
+    kr[0] = buf_load<sizeof(KT)>(r, off);
   }
-  __device__ static h8_t kfrag(const uint32_t (&kd)[KDW], int i) {
+  __device__ static h8_t kfrag(const KT (&kr)[KL], int i) {
     h2_t h[4];
-    i4x8_to_h2x4(kd[i], h);
+    i4x8_to_h2x4(kr[0][i], h);
     return h8_t{h[0].x, h[0].y, h[1].x, h[1].y, h[2].x, h[2].y, h[3].x, h[3].y};
   }
   // slot e of step i holds element 8 i + {0,2,4,6,1,3,5,7}[e] of the lane's run
   __host__ __device__ static constexpr int kd_index(int i, int kb, int e) {
     return (D / 4) * kb + 8 * i + (e < 4 ? 2 * e : 2 * (e - 4) + 1);
+  }
+  __device__ static h8_t qfrag(rsrc_t rq, uint32_t row_elem, int i, int kb) {
+    const h8_t v = __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
+    return h8_t{v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]};
   }
   static constexpr int VB = (D == 128) ? 16 : 8;
   static constexpr int LPR = ROWB / VB;  // 4
@@ -182,7 +208,8 @@ struct Fmt<KV_I4, D> {
   static constexpr int VLD = 16 / TPL;   // 1
   static constexpr int EV = 2 * VB;
   static constexpr float VBIAS = 8.0f;   // vconv yields n + 8
-  __device__ static void vconv(const uint32_t (&vd)[VB / 4], float (&f)[EV]) {
+  template <typename VT>
+  __device__ static void vconv(const VT vd, float (&f)[EV]) {
 #pragma unroll
     for (int k = 0; k < VB / 4; ++k) {
       const uint32_t t = vd[k] ^ 0x88888888u;
@@ -198,16 +225,12 @@ struct Fmt<KV_I4, D> {
   __host__ __device__ static constexpr int vd_index(int lir, int e) { return EV * lir + e; }
 };
 
+template <int VB>
+using vraw_t = typename std::conditional<VB == 16, u4_t, u2_t>::type;
+
 template <int FMT, int D>
-__device__ __forceinline__ void load_v(const uint8_t* row, int lir, uint32_t (&vd)[Fmt<FMT, D>::VB / 4]) {
-  using F = Fmt<FMT, D>;
-  if constexpr (F::VB == 16) {
-    const u4_t v = *reinterpret_cast<const u4_t*>(row + 16 * lir);
-    vd[0] = v.x; vd[1] = v.y; vd[2] = v.z; vd[3] = v.w;
-  } else {
-    const u2_t v = *reinterpret_cast<const u2_t*>(row + 8 * lir);
-    vd[0] = v.x; vd[1] = v.y;
-  }
+__device__ __forceinline__ vraw_t<Fmt<FMT, D>::VB> load_v(rsrc_t r, uint32_t off) {
+  return buf_load<Fmt<FMT, D>::VB>(r, off);
 }
 
 }  // namespace fqkv

@@ -16,7 +16,7 @@ and call ``m.<function>(...)``; :func:`load` returns the module that serves
 all five, so ``m = load(name="t_fp16", sources=[...])`` keeps working.
 
 The functions run hand-written HIP kernels from ``libfqkv_decode.so``; there
-is no CPU or PyTorch fallback. Importing this package raises ImportError if
+is no CPU or PyTorch fallback: using any entry point raises ImportError if
 the native libraries are not built (``python -m fqkv_decode._build``).
 """
 
@@ -25,7 +25,7 @@ import os
 
 import torch  # noqa: F401  (binds the HIP runtime PyTorch ships before ours loads)
 
-from ._build import EXT_NAME, LIB_NAME, PKG_DIR, ext_filename
+from ._paths import EXT_NAME, LIB_NAME, PKG_DIR, ext_filename
 
 __all__ = [
     "decode_attn_fp16_mw",
@@ -37,6 +37,10 @@ __all__ = [
     "lib_path",
     "ext_path",
 ]
+
+_ENTRY_POINTS = ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa",
+                 "gqa_sk_fast")
+_EXT = None
 
 
 def lib_path():
@@ -50,6 +54,10 @@ def ext_path():
 
 
 def _load_ext():
+    """Import the PyTorch binding (once); ImportError if the native libraries are not built."""
+    global _EXT
+    if _EXT is not None:
+        return _EXT
     path = ext_path()
     if not os.path.exists(path) or not os.path.exists(lib_path()):
         raise ImportError(
@@ -58,16 +66,18 @@ def _load_ext():
     spec = importlib.util.spec_from_file_location("fqkv_decode." + EXT_NAME, path)
     mod = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mod)
+    _EXT = mod
     return mod
 
 
-_ext = _load_ext()
-
-decode_attn_fp16_mw = _ext.decode_attn_fp16_mw
-decode_attn_int8_mw = _ext.decode_attn_int8_mw
-decode_attn_int4 = _ext.decode_attn_int4
-decode_attn_gqa = _ext.decode_attn_gqa
-gqa_sk_fast = _ext.gqa_sk_fast
+def __getattr__(name):
+    # The entry points resolve to the native module on first use, so the
+    # package (and its build step) imports before the libraries exist.
+    if name in _ENTRY_POINTS:
+        return getattr(_load_ext(), name)
+    if name == "_ext":
+        return _load_ext()
+    raise AttributeError("module 'fqkv_decode' has no attribute %r" % name)
 
 
 def load(name=None, sources=None, extra_cuda_cflags=None, verbose=False, **kwargs):
@@ -79,7 +89,7 @@ def load(name=None, sources=None, extra_cuda_cflags=None, verbose=False, **kwarg
     which exposes all five entry points; the arguments are accepted and
     ignored.
     """
-    return _ext
+    return _load_ext()
 
 
 def choose_splits(rows, G, N, D, kv_format, W):
@@ -87,9 +97,9 @@ def choose_splits(rows, G, N, D, kv_format, W):
 
     ``kv_format`` is 0 (fp16), 1 (int8) or 2 (int4).
     """
-    return _ext._choose_splits(rows, G, N, D, kv_format, W)
+    return _load_ext()._choose_splits(rows, G, N, D, kv_format, W)
 
 
 def cu_count():
     """Compute units of the current HIP device."""
-    return _ext._cu_count()
+    return _load_ext()._cu_count()

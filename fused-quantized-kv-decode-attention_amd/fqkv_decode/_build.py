@@ -17,16 +17,14 @@ import subprocess
 import sys
 import sysconfig
 
-PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+from ._paths import EXT_NAME, LIB_NAME, PKG_DIR, ext_filename
+
 ROOT = os.path.dirname(PKG_DIR)  # fused-quantized-kv-decode-attention_amd/
 CSRC = os.path.join(ROOT, "csrc")
 INCLUDE = os.path.join(os.path.dirname(ROOT), "include")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 ARCH = "gfx950"
-
-LIB_NAME = "libfqkv_decode.so"
-EXT_NAME = "_fqkv_torch"
 
 # Every HIP translation unit: gfx950 only, -O3, and no packed-fp32 VALU
 # instructions (v_pk_{add,mul,fma}_f32 are disabled on this target).
@@ -35,10 +33,6 @@ HIP_FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Wno-unused-result",
 ]
-
-
-def ext_filename():
-    return EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX")
 
 
 def _run(cmd, verbose):
