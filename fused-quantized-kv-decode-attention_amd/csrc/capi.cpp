@@ -37,6 +37,16 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
+// Split merge: in-kernel (arrival counters; one kernel per call) unless
+// forced to the two-kernel form or the call has too many head groups.
+std::atomic<int> g_force_two_kernel{0};
+std::atomic<unsigned> g_slot_ticket{0};
+
+int merge_slot(int64_t groups) {
+  if (g_force_two_kernel.load(std::memory_order_relaxed) || groups > MAX_SPLIT_GROUPS) return -1;
+  return (int)(g_slot_ticket.fetch_add(1, std::memory_order_relaxed) % SPLIT_SLOTS);
+}
+
 // CU count per device, queried once (256 on MI355X).
 constexpr int MAX_DEV = 64;
 std::atomic<int> g_cus[MAX_DEV];
@@ -78,8 +88,11 @@ int64_t splits_for(int64_t rows, int64_t G, int64_t N, int fmt, int64_t W, int c
   return S < 1 ? 1 : S;
 }
 
+// Internal split scratch: m [heads*S], l [heads*S], then acc [heads*S*D]
+// starting on a 16-byte boundary (the combine kernel reads it as float4).
+size_t acc_offset_floats(int64_t heads, int64_t S) { return (size_t)((2 * heads * S + 3) & ~(int64_t)3); }
 size_t scratch_bytes(int64_t heads, int64_t S, int64_t D) {
-  return (size_t)heads * (size_t)S * (size_t)(D + 2) * sizeof(float);
+  return (acc_offset_floats(heads, S) + (size_t)heads * (size_t)S * (size_t)D) * sizeof(float);
 }
 
 int check_common(int64_t N, int64_t D, int64_t W) {
@@ -102,7 +115,8 @@ int run_decode(int fmt, const void* q, const void* K, const void* V, const void*
   const int64_t heads = rows * G;
   int64_t S = splits_for(rows, G, N, fmt, W, cus);
   if (S > 1 && (ws == nullptr || scratch_bytes(heads, S, D) > ws_bytes)) {
-    const int64_t fit = ws ? (int64_t)(ws_bytes / scratch_bytes(heads, 1, D)) : 0;
+    int64_t fit = ws ? (int64_t)(ws_bytes / scratch_bytes(heads, 1, D)) : 0;
+    while (fit >= 2 && scratch_bytes(heads, fit, D) > ws_bytes) --fit;
     S = fit >= 2 ? (fit < S ? fit : S) : 1;
   }
   if (S > 1 && !aligned(ws, 16)) return fail(FQKV_ERR_ARG, "workspace must be 16-byte aligned");
@@ -124,15 +138,17 @@ int run_decode(int fmt, const void* q, const void* K, const void* V, const void*
   p.scale = 1.0f / sqrtf((float)D);
   p.c = p.scale * 1.4426950408889634f;
   p.direct = S == 1;
+  p.slot = -1;
   if (!p.direct) {
     float* f = (float*)ws;
     p.m_part = f;
     p.l_part = f + heads * S;
-    p.o_part = f + 2 * heads * S;
+    p.o_part = f + acc_offset_floats(heads, S);
+    p.slot = merge_slot(rows * ngroups);
   }
   hipError_t e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)W, st);
   if (e != hipSuccess) return hip_fail(e, "launch: partial kernel");
-  if (!p.direct) {
+  if (!p.direct && p.slot < 0) {
     e = launch_combine((int)D, p.m_part, p.l_part, p.o_part, o, (int)heads, (int)S, 4, st);
     if (e != hipSuccess) return hip_fail(e, "launch: combine kernel");
   }
@@ -168,7 +184,7 @@ int sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l
   if (rc) return rc;
   if ((rc = check_span(N, D, KV_F16))) return rc;
   if (!m_part || !l_part || !o_part) return fail(FQKV_ERR_ARG, "null scratch pointer");
-  if (!aligned(o_part, 8)) return fail(FQKV_ERR_ARG, "o_part must be 8-byte aligned");
+  if (!aligned(o_part, 16)) return fail(FQKV_ERR_ARG, "o_part must be 16-byte aligned");
   const int64_t G = Hq / Hkv;
   const int hg = choose_hg(G, KV_F16);
   const int64_t ngroups = (G + hg - 1) / hg;
@@ -190,14 +206,20 @@ int sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l
   p.ngroups = (int)ngroups;
   p.scale = 1.0f / sqrtf((float)D);
   p.c = p.scale * 1.4426950408889634f;
+  p.o = (_Float16*)o;
   p.direct = 0;
+  // S == 1 still writes the scratch (the caller asked for it); one split needs
+  // no merge beyond the workgroup's own, done by the two-kernel path's combine.
+  p.slot = S > 1 ? merge_slot(Hkv * ngroups) : -1;
   hipError_t e;
   if (ev_begin && (e = hipEventRecord((hipEvent_t)ev_begin, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
   e = launch_partial(KV_F16, (int)D, hg, p, (int)nblocks, (int)W, st);
   if (e != hipSuccess) return hip_fail(e, "partial");
   if (ev_end && (e = hipEventRecord((hipEvent_t)ev_end, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-  e = launch_combine((int)D, m_part, l_part, o_part, o, (int)Hq, (int)S, (int)CW, st);
-  if (e != hipSuccess) return hip_fail(e, "combine");
+  if (p.slot < 0) {
+    e = launch_combine((int)D, m_part, l_part, o_part, o, (int)Hq, (int)S, (int)CW, st);
+    if (e != hipSuccess) return hip_fail(e, "combine");
+  }
   return FQKV_OK;
 }
 
@@ -208,6 +230,11 @@ extern "C" {
 const char* fqkv_last_error(void) { return g_err; }
 
 const char* fqkv_version(void) { return "fqkv_decode 0.1.0 (gfx950)"; }
+
+int fqkv_set_two_kernel_merge(int enable) {
+  g_force_two_kernel.store(enable ? 1 : 0, std::memory_order_relaxed);
+  return FQKV_OK;
+}
 
 int fqkv_device_cu_count(int* cu_count) {
   if (!cu_count) return fail(FQKV_ERR_ARG, "null cu_count");

@@ -61,10 +61,144 @@ __device__ __forceinline__ float row16_sum(float x) {
   return x;
 }
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// Sum of x over the lanes of the wave that share (lane % LPR): rotations
+// within each 16-lane row for LPR < 16, then v_permlane16_swap (rows 0+1,
+// 2+3) and v_permlane32_swap (halves). Adding both swap outputs makes the
+// result independent of which operand receives which half. All VALU.
+template <int LPR>
+__device__ __forceinline__ float sum_over_token_rows(float x) {
+  if constexpr (LPR <= 4) x += dpp<0x124>(x);  // row_ror:4
+  if constexpr (LPR <= 8) x += dpp<0x128>(x);  // row_ror:8
+  // (swap results are copied to scalars before the bit casts: this
+  // compiler's __builtin_bit_cast of a vector element reads element 0)
+  const unsigned u = __builtin_bit_cast(unsigned, x);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const unsigned a = r16[0], b = r16[1];
+  x = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
+  const unsigned v = __builtin_bit_cast(unsigned, x);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  const unsigned c = r32[0], d = r32[1];
+  return __builtin_bit_cast(float, c) + __builtin_bit_cast(float, d);
+}
 __device__ __forceinline__ float readlane_f(float x, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
 }
 __device__ __forceinline__ void compiler_fence() { __asm__ __volatile__("" ::: "memory"); }
+
+typedef float fl4_t __attribute__((ext_vector_type(4)));
+
+// Arrival counters of the in-kernel split merge. Zero at load; the workgroup
+// that merges a group resets its counter, so every call leaves them at zero.
+__device__ int g_split_arrivals[SPLIT_SLOTS][MAX_SPLIT_GROUPS];
+
+// Merge S split partials for query heads h0 .. h0+nh-1 with the whole
+// workgroup: o[h] = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s
+// (decode_attn_gqa_sk_fast.cu:57-94; m in natural-log units, an empty split
+// has m = -inf and weight 0). Thread t owns float4 column c of head hh for
+// splits g, g + NG, ...; it issues a chunk of CH splits' loads before the
+// block-wide maximum is known, so a merge costs about one memory round trip.
+// s_acc holds blockDim.x float4, s_red 2 * blockDim.x / (D/4) floats.
+// COHERENT: read the partials with device-scope (sc1) loads, for partials
+// that other workgroups of the same launch stored with device-scope stores.
+template <int D, bool COHERENT>
+__device__ void merge_splits(const float* __restrict__ m_part, const float* __restrict__ l_part,
+                             const float* __restrict__ o_part, _Float16* __restrict__ o, size_t h0,
+                             int nh, int S, fl4_t* s_acc, float* s_red) {
+  constexpr int C4 = D / 4;
+  constexpr int CH = 8;
+  auto ld1 = [](const float* ptr) -> float {
+    if constexpr (COHERENT) return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *ptr;
+  };
+  // one descriptor (uniform) over the acc partials of heads h0 .. h0+nh-1
+  const rsrc_t rO = make_rsrc(o_part + h0 * S * D, (uint32_t)(nh * S * D) * 4u);
+  auto ld4 = [&](const fl4_t* base, uint32_t idx) -> fl4_t {
+    if constexpr (COHERENT) {
+      const uint32_t off = (uint32_t)((const float*)(base + idx) - (o_part + h0 * S * D)) * 4u;
+      return __builtin_bit_cast(fl4_t, __builtin_amdgcn_raw_buffer_load_b128(rO, (int)off, 0, CPOL_SC1));
+    } else {
+      return base[idx];
+    }
+  };
+  const int t = threadIdx.x;
+  const int nt = blockDim.x;
+  const int hpr = nt / C4;  // heads per round (>= 4: nt >= 128, C4 <= 32)
+  float* s_mx = s_red;
+  float* s_l = s_red + hpr;
+  for (int hb = 0; hb < nh; hb += hpr) {
+    const int hr = min(hpr, nh - hb);
+    const int NG = nt / (C4 * hr);
+    const int c = t % C4;
+    const int hh = (t / C4) % hr;
+    const int g = t / (C4 * hr);
+    const bool act = g < NG;
+    const size_t h = h0 + hb + hh;
+    const float* mh = m_part + h * S;
+    const float* lh = l_part + h * S;
+    const fl4_t* oh = reinterpret_cast<const fl4_t*>(o_part + h * S * D);
+    fl4_t ov[CH];
+    float mv[CH], lv[CH];
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const int sk = g + k * NG;
+      const bool ok = act && sk < S;
+      ov[k] = ok ? ld4(oh, (uint32_t)(sk * C4 + c)) : fl4_t{0.0f, 0.0f, 0.0f, 0.0f};
+      mv[k] = ok ? ld1(mh + sk) : -INFINITY;
+      lv[k] = ok ? ld1(lh + sk) : 0.0f;
+    }
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < CH; ++k) mloc = fmaxf(mloc, mv[k]);
+    if (act)
+      for (int sk = g + CH * NG; sk < S; sk += NG) mloc = fmaxf(mloc, ld1(mh + sk));
+    if (act && c == 0) s_mx[g * hr + hh] = mloc;
+    __syncthreads();
+    float M = -INFINITY;
+    for (int gg = 0; gg < NG; ++gg) M = fmaxf(M, s_mx[gg * hr + hh]);
+    fl4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float L = 0.0f;
+    if (act && M != -INFINITY) {
+      for (int base = 0;; base += CH * NG) {
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          const float sc = fast_exp2((mv[k] - M) * LOG2E);
+          L += sc * lv[k];
+          acc += sc * ov[k];
+        }
+        const int nb = base + CH * NG;
+        if (nb >= S) break;
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          const int sk = nb + g + k * NG;
+          const bool ok = sk < S;
+          ov[k] = ok ? ld4(oh, (uint32_t)(sk * C4 + c)) : fl4_t{0.0f, 0.0f, 0.0f, 0.0f};
+          mv[k] = ok ? ld1(mh + sk) : -INFINITY;
+          lv[k] = ok ? ld1(lh + sk) : 0.0f;
+        }
+      }
+    }
+    s_acc[t] = acc;
+    if (act && c == 0) s_l[g * hr + hh] = L;
+    __syncthreads();
+    if (t < hr * C4) {
+      const int oh2 = t / C4;
+      const int c2 = t % C4;
+      fl4_t r = {0.0f, 0.0f, 0.0f, 0.0f};
+      float Lt = 0.0f;
+      for (int gg = 0; gg < NG; ++gg) {
+        r += s_acc[(gg * hr + oh2) * C4 + c2];
+        Lt += s_l[gg * hr + oh2];
+      }
+      r /= Lt;
+      _Float16* dst = o + (h0 + hb + oh2) * D + 4 * c2;
+      dst[0] = (_Float16)r.x;
+      dst[1] = (_Float16)r.y;
+      dst[2] = (_Float16)r.z;
+      dst[3] = (_Float16)r.w;
+    }
+    __syncthreads();
+  }
+}
 
 template <int FMT, int D, int HG>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
@@ -75,6 +209,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   __shared__ float s_o[NW_MAX][HG][D];
   __shared__ float s_m[NW_MAX][HG];
   __shared__ float s_l[NW_MAX][HG];
+  __shared__ float s_sc[NW_MAX][HG];  // per-wave merge weights e^(m_w - M)
+  __shared__ float s_L[HG];
+  __shared__ float s_M[HG];
+  __shared__ fl4_t s_macc[64 * NW_MAX];        // in-kernel split merge
+  __shared__ float s_mred[2 * 64 * NW_MAX / (D / 4)];
+  __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
   // wave index as a scalar, so tile loops branch per wave, not per lane
@@ -228,12 +368,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
   for (int h = 0; h < HG; ++h)
 #pragma unroll
-    for (int e = 0; e < F::EV; ++e) {
-      float v = acc[h][e];
-#pragma unroll
-      for (int x = F::LPR; x < 64; x <<= 1) v += __shfl_xor(v, x);
-      acc[h][e] = v;
-    }
+    for (int e = 0; e < F::EV; ++e) acc[h][e] = sum_over_token_rows<F::LPR>(acc[h][e]);
   if constexpr (F::QUANT) {
 #pragma unroll
     for (int h = 0; h < HG; ++h) {
@@ -261,89 +396,84 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   __syncthreads();
 
   // ---- merge the waves, emit output or split scratch ----
+  // One thread per head first turns the waves' maxima into merge weights
+  // (an empty wave, m = -inf, gets weight 0; an all-empty split keeps M = -inf).
+  if (threadIdx.x < hcnt) {
+    const int h = threadIdx.x;
+    float M = -INFINITY;
+    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_m[ww][h]);
+    float L = 0.0f;
+    for (int ww = 0; ww < nw; ++ww) {
+      const float sc = (M == -INFINITY) ? 0.0f : fast_exp2((s_m[ww][h] - M) * p.c);
+      s_sc[ww][h] = sc;
+      L += sc * s_l[ww][h];
+    }
+    s_M[h] = M;
+    s_L[h] = L;
+  }
+  __syncthreads();
   for (int idx = threadIdx.x; idx < hcnt * D; idx += blockDim.x) {
     const int h = idx / D;
     const int d = idx - h * D;
-    float M = -INFINITY;
-    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_m[ww][h]);
-    float L = 0.0f, O = 0.0f;
-    if (M != -INFINITY) {
-      for (int ww = 0; ww < nw; ++ww) {
-        const float sc = fast_exp2((s_m[ww][h] - M) * p.c);
-        L += sc * s_l[ww][h];
-        O += sc * s_o[ww][h][d];
-      }
-    }
+    const float M = s_M[h];
+    const float L = s_L[h];
+    float O = 0.0f;
+    for (int ww = 0; ww < nw; ++ww) O += s_sc[ww][h] * s_o[ww][h][d];
     const size_t qh = qrow0 + h;
     if (p.direct) {
       p.o[qh * D + d] = (_Float16)(O / L);
     } else {
       const size_t b = qh * p.S + s;
-      if (d == 0) {
-        p.m_part[b] = (M == -INFINITY) ? -INFINITY : M * p.scale;
-        p.l_part[b] = L;
+      const float mo = (M == -INFINITY) ? -INFINITY : M * p.scale;
+      if (p.slot >= 0) {  // device-scope stores: read by another workgroup of this launch
+        if (d == 0) {
+          __hip_atomic_store(p.m_part + b, mo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(p.l_part + b, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __hip_atomic_store(p.o_part + b * D + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        if (d == 0) {
+          p.m_part[b] = mo;
+          p.l_part[b] = L;
+        }
+        p.o_part[b * D + d] = O;
       }
-      p.o_part[b * D + d] = O;
     }
+  }
+
+  // ---- in-kernel split merge: the last of the S workgroups of this
+  // (KV row, head group) merges the S partials of its heads. The partials
+  // above were stored at device scope (sc1, past the non-coherent per-XCD
+  // L2s); each thread waits for its stores to complete before the barrier,
+  // so by the time thread 0 counts the workgroup in, its partials are
+  // visible device-wide. The last arriver reads every partial with
+  // device-scope loads. No L2 writeback or invalidate is needed, and nobody
+  // waits on the counter, so no workgroup can stall.
+  if (!p.direct && p.slot >= 0) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      int* ctr = &g_split_arrivals[p.slot][blockIdx.x / p.S];
+      const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = prev == p.S - 1;
+      if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      s_last = last;
+    }
+    __syncthreads();
+    if (s_last) merge_splits<D, true>(p.m_part, p.l_part, p.o_part, p.o, qrow0, hcnt, p.S, s_macc, s_mred);
   }
 }
 
-// Merge S split partials of one query head per workgroup:
-// o = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s (decode_attn_gqa_sk_fast.cu:57-94).
-// Every thread first reduces M; wave w then takes splits w, w + nw, ...
-// with lanes covering the head dimension (D/64 floats each); waves meet in LDS.
+// Two-kernel form of the split merge (decode_attn_gqa_sk_fast.cu:57-94): one
+// workgroup per query head. Used when a call cannot take arrival counters.
 template <int D>
 __global__ void __launch_bounds__(64 * NW_MAX) combine_kernel(const float* __restrict__ m_part,
                                                               const float* __restrict__ l_part,
                                                               const float* __restrict__ o_part,
                                                               _Float16* __restrict__ o, int S) {
-  constexpr int E = D / 64;
-  __shared__ float s_red[NW_MAX];
-  __shared__ float s_l[NW_MAX];
-  __shared__ float s_o[NW_MAX][D];
-  const int h = blockIdx.x;
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int nw = blockDim.x >> 6;
-  const float* mh = m_part + (size_t)h * S;
-  const float* lh = l_part + (size_t)h * S;
-  const float* oh = o_part + (size_t)h * S * D;
-
-  float M = -INFINITY;
-  for (int s = threadIdx.x; s < S; s += blockDim.x) M = fmaxf(M, mh[s]);
-#pragma unroll
-  for (int x = 32; x > 0; x >>= 1) M = fmaxf(M, __shfl_xor(M, x));
-  if (lane == 0) s_red[w] = M;
-  __syncthreads();
-  M = -INFINITY;
-  for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_red[ww]);
-
-  float L = 0.0f, O[E];
-#pragma unroll
-  for (int e = 0; e < E; ++e) O[e] = 0.0f;
-  if (M != -INFINITY) {
-    for (int s = w; s < S; s += nw) {
-      const float sc = fast_exp2((mh[s] - M) * LOG2E);  // empty split: m = -inf -> 0
-      L += sc * lh[s];
-      const float* src = oh + (size_t)s * D + lane * E;
-#pragma unroll
-      for (int e = 0; e < E; ++e) O[e] += sc * src[e];
-    }
-  }
-  if (lane == 0) s_l[w] = L;
-#pragma unroll
-  for (int e = 0; e < E; ++e) s_o[w][lane * E + e] = O[e];
-  __syncthreads();
-  if (w == 0) {
-    float Lt = 0.0f;
-    for (int ww = 0; ww < nw; ++ww) Lt += s_l[ww];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      float Ot = 0.0f;
-      for (int ww = 0; ww < nw; ++ww) Ot += s_o[ww][lane * E + e];
-      o[(size_t)h * D + lane * E + e] = (_Float16)(Ot / Lt);
-    }
-  }
+  __shared__ fl4_t s_acc[64 * NW_MAX];
+  __shared__ float s_red[2 * 64 * NW_MAX / (D / 4)];
+  merge_splits<D, false>(m_part, l_part, o_part, o, blockIdx.x, 1, S, s_acc, s_red);
 }
 
 // Dequantise through the kernels' own conversions (K side: int -> fp16

@@ -71,6 +71,7 @@ __device__ __forceinline__ float ubyte_f(uint32_t w, int k) {
 // Raw buffer access (gfx9 descriptor word 3 = 0x00020000, stride 0):
 // loads whose byte offset is at or past num_records return zeros.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int CPOL_SC1 = 16;  // cache-policy bit: device-scope coherent access
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }

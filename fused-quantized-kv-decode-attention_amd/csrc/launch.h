@@ -29,7 +29,13 @@ struct PartialParams {
   float c;               // softmax scale * log2(e)
   float scale;           // softmax scale (natural-log units for m_part)
   int direct;            // 1: S == 1, write normalised fp16 output
+  int slot;              // !direct: arrival-counter slot for the in-kernel merge, -1 = none
 };
+
+// In-kernel split merge: each call with S > 1 takes one of SPLIT_SLOTS slots
+// of MAX_SPLIT_GROUPS arrival counters (one per (KV row, head group)).
+constexpr int SPLIT_SLOTS = 16;
+constexpr int MAX_SPLIT_GROUPS = 16384;
 
 hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& p, int nblocks, int nw,
                           hipStream_t st);

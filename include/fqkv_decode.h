@@ -6,7 +6,8 @@
  * contiguous memory, every size is a 64-bit integer, `stream` is a
  * hipStream_t passed as void* (NULL = the legacy default stream). All calls
  * are asynchronous on `stream`; none synchronises the device and none
- * allocates device memory (callers pass any workspace).
+ * allocates device memory (callers pass any workspace; the library's only
+ * device state is a static array of split-merge arrival counters).
  *
  * Data formats (the reference's layouts, unchanged):
  *   fp16 KV        K, V: [rows, N, D] __half, row-major
@@ -16,6 +17,9 @@
  *                  decodes as n - 16 when n >= 8; scales as for int8
  *   dequantised value = (float)q * (float)scale, exact in fp32
  *   softmax scale  = 1.0f / sqrtf((float)D); D (head_dim) is 64 or 128
+ *
+ * Alignment: q, K, V and o_part 16 bytes (K, V 8 bytes for int4 at D = 64);
+ * o, scales 2 bytes. Each K or V row block (N rows) must span < 4 GiB.
  *
  * Return value: FQKV_OK (0) on success; otherwise a non-zero FQKV_ERR_* code
  * and fqkv_last_error() describes the failure (thread-local). Argument
@@ -134,6 +138,20 @@ int fqkv_gqa_sk_fast_timed(const void* q, const void* K, const void* V, float* m
  */
 int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, int64_t D,
                     int kv_format, int path, void* stream);
+
+/*
+ * Split merge mode for calls that split the sequence (gqa_sk_fast with S > 1
+ * and the internal splits of the single-block entry points). Default (0):
+ * one kernel per call; the last workgroup of each head group to finish merges
+ * that group's split partials, using library-owned arrival counters (16
+ * slots taken round-robin per call, so up to 16 such calls may run
+ * concurrently on different streams; calls that replay one captured graph
+ * concurrently share a slot and must not overlap). 1: a partial kernel then
+ * a separate combine kernel, as the reference launches them
+ * (decode_attn_gqa_sk_fast.cu:100-111). Results agree to fp32 rounding.
+ * Process-wide; returns FQKV_OK.
+ */
+int fqkv_set_two_kernel_merge(int enable);
 
 /* Number of compute units of the current device (used by the split heuristic). */
 int fqkv_device_cu_count(int* cu_count);

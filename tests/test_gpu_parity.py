@@ -56,7 +56,7 @@ def test_fp16_mha(B, N, W, D):
     assert maxerr(out, oracle.attention(q.numpy(), K.numpy(), V.numpy())) <= TOL
 
 
-def test_fp16_mha_long_sequence_uses_splits():
+def test_fp16_mha_long_sequence_uses_splits(merge_mode):
     B, N, D = 2, 16384, 128
     assert fq.choose_splits(B, 1, N, D, 0, 8) > 1
     g = torch.Generator().manual_seed(0)
@@ -184,6 +184,14 @@ def test_gqa_equals_repeat_kv_plus_mha():
 
 # --------------------------------------------------------------- split-K ----
 
+@pytest.fixture(params=["fused", "two_kernel"])
+def merge_mode(request):
+    """Split merge inside the partial kernel (default) or as a separate combine kernel."""
+    fq._ext._set_two_kernel_merge(request.param == "two_kernel")
+    yield request.param
+    fq._ext._set_two_kernel_merge(False)
+
+
 def run_sk(q, K, V, S, W, CW):
     Hq, D = q.shape
     mp = torch.full((Hq, S), float("nan"), device=DEV)
@@ -197,7 +205,7 @@ def run_sk(q, K, V, S, W, CW):
 @pytest.mark.parametrize("N,D,S,W,CW", [(1024, 64, 8, 8, 4), (4096, 128, 16, 8, 4), (16384, 64, 64, 8, 8),
                                         (3, 128, 8, 4, 4), (1, 64, 4, 2, 4), (100, 64, 7, 4, 4),
                                         (16384, 128, 128, 8, 8), (512, 128, 16, 2, 8), (32768, 128, 64, 4, 4)])
-def test_gqa_sk_fast_reference_cases(N, D, S, W, CW):
+def test_gqa_sk_fast_reference_cases(N, D, S, W, CW, merge_mode):
     Hq, Hkv = 32, 8
     g = torch.Generator().manual_seed(0)
     q, K, V = draw(g, Hq, D).half(), draw(g, Hkv, N, D).half(), draw(g, Hkv, N, D).half()
@@ -207,7 +215,7 @@ def test_gqa_sk_fast_reference_cases(N, D, S, W, CW):
 
 
 @pytest.mark.parametrize("N,S", [(100, 7), (3, 8), (1000, 16), (1, 1)])
-def test_gqa_sk_fast_scratch_layout(N, S):
+def test_gqa_sk_fast_scratch_layout(N, S, merge_mode):
     """m_part / l_part / o_part hold the reference's per-split (m, l, acc), empty splits (-inf, 0, 0)."""
     Hq, Hkv, D = 8, 2, 128
     g = torch.Generator().manual_seed(8)
@@ -223,7 +231,7 @@ def test_gqa_sk_fast_scratch_layout(N, S):
     assert maxerr(o, oracle.combine_partials(m, l, acc)) <= TOL
 
 
-def test_gqa_sk_fast_knob_invariance():
+def test_gqa_sk_fast_knob_invariance(merge_mode):
     Hq, Hkv, N, D = 32, 8, 5000, 128
     g = torch.Generator().manual_seed(9)
     q, K, V = draw(g, Hq, D).half(), draw(g, Hkv, N, D).half(), draw(g, Hkv, N, D).half()
@@ -234,7 +242,7 @@ def test_gqa_sk_fast_knob_invariance():
                 assert maxerr(run_sk(q, K, V, S, W, CW)[0], ref) <= TOL, (S, W, CW)
 
 
-def test_gqa_sk_fast_batch_folds_into_heads():
+def test_gqa_sk_fast_batch_folds_into_heads(merge_mode):
     """Batch B as q [B*Hq, D], K [B*Hkv, N, D]: head b*Hq+j reads KV row b*Hkv + j/G."""
     B, Hq, Hkv, N, D = 3, 32, 8, 2048, 128
     g = torch.Generator().manual_seed(10)
@@ -244,6 +252,20 @@ def test_gqa_sk_fast_batch_folds_into_heads():
     assert maxerr(o, ref) <= TOL
     o2 = fq.decode_attn_gqa(gpu(q), gpu(K), gpu(V), 8).reshape(B * Hq, D)
     assert float((o.float() - o2.float()).abs().max()) <= TOL
+
+
+def test_split_merge_many_calls_in_a_row():
+    """More consecutive split calls than arrival-counter slots, with changing
+    shapes: every result stays correct (counters are reset by each merge)."""
+    g = torch.Generator().manual_seed(12)
+    cases = []
+    for i, (Hq, Hkv, N, S) in enumerate([(32, 8, 1000, 16), (8, 2, 100, 7), (64, 8, 3000, 33), (4, 1, 50, 50)] * 6):
+        q, K, V = draw(g, Hq, 128).half(), draw(g, Hkv, N, 128).half(), draw(g, Hkv, N, 128).half()
+        ref = oracle.gqa_attention(q.numpy()[None], K.numpy()[None], V.numpy()[None])[0]
+        cases.append((run_sk(q, K, V, S, 4, 8)[0], ref))
+    torch.cuda.synchronize()
+    for o, ref in cases:
+        assert maxerr(o, ref) <= TOL
 
 
 # --------------------------------------------------------- golden files ----
