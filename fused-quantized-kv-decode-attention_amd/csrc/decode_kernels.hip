@@ -205,13 +205,10 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   using F = Fmt<FMT, D>;
   constexpr int U = 4;
   constexpr int NR = (HG + 3) / 4;  // MFMA result registers that carry heads
-  __shared__ float s_w[NW_MAX][16][HG];
+  __shared__ float s_w[NW_MAX][U][16][HG];
   __shared__ float s_o[NW_MAX][HG][D];
-  __shared__ float s_m[NW_MAX][HG];
-  __shared__ float s_l[NW_MAX][HG];
-  __shared__ float s_sc[NW_MAX][HG];  // per-wave merge weights e^(m_w - M)
-  __shared__ float s_L[HG];
-  __shared__ float s_M[HG];
+  __shared__ float s_m[HG][NW_MAX];
+  __shared__ float s_l[HG][NW_MAX];
   __shared__ fl4_t s_macc[64 * NW_MAX];        // in-kernel split merge
   __shared__ float s_mred[2 * 64 * NW_MAX / (D / 4)];
   __shared__ int s_last;
@@ -266,11 +263,6 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
     for (int e = 0; e < F::EV; ++e) acc[h][e] = 0.0f;
 
-  struct Tile {
-    typename F::KT kr[F::KL];
-    vraw_t<F::VB> vr[F::VLD];
-    float ksc, vsc;
-  };
   // Buffer descriptors end at the split's last token, so rows past it read
   // as zeros (their scores are masked); offsets are 32-bit from the row block.
   const uint32_t nbytes = (uint32_t)hi * F::ROWB;
@@ -280,41 +272,77 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   const rsrc_t rVs = make_rsrc(Vsr, 2u * (uint32_t)hi);
   const uint32_t koff = (uint32_t)kt * F::ROWB + F::klane(kb);
   const uint32_t voff = (uint32_t)vt * F::ROWB + (uint32_t)vl * F::VB;
-  auto load_tile = [&](Tile& t, int tb) {
-    const uint32_t base = (uint32_t)tb * F::ROWB;
-    F::load_k(rK, base + koff, t.kr);
-    if constexpr (F::QUANT) {
-      t.ksc = (float)__builtin_bit_cast(_Float16, buf_load<2>(rKs, 2u * (uint32_t)(tb + kt)));
-      t.vsc = (float)__builtin_bit_cast(_Float16, buf_load<2>(rVs, 2u * (uint32_t)(tb + kt)));
-    } else {
-      t.ksc = 1.0f;
-      t.vsc = 1.0f;
+
+  // Each pass covers U tiles of this wave (tiles interleave across waves).
+  // All K loads of the pass are issued, then all V loads, before anything is
+  // consumed: straight-line code, so the load counter waits exactly for the
+  // data about to be used while the rest is still arriving. The pass then
+  // scores all U tiles with the matrix cores, takes ONE online-softmax step
+  // over its 16 U tokens per row (one max reduction, one rescale), and
+  // accumulates p * V.
+  const int step = 16 * nw;
+  for (int pb = lo + 16 * w; pb < hi; pb += U * step) {
+    typename F::KT kr[U][F::KL];
+    vraw_t<F::VB> vr[U][F::VLD];
+    float ksc[U], vsc[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const uint32_t base = (uint32_t)(pb + u * step) * F::ROWB;
+      F::load_k(rK, base + koff, kr[u]);
+      if constexpr (F::QUANT) {
+        const uint32_t so = 2u * (uint32_t)(pb + u * step + kt);
+        ksc[u] = (float)__builtin_bit_cast(_Float16, buf_load<2>(rKs, so));
+        vsc[u] = (float)__builtin_bit_cast(_Float16, buf_load<2>(rVs, so));
+      } else {
+        ksc[u] = 1.0f;
+        vsc[u] = 1.0f;
+      }
     }
 #pragma unroll
-    for (int j = 0; j < F::VLD; ++j) t.vr[j] = load_v<FMT, D>(rV, base + voff + (uint32_t)(j * F::TPL * F::ROWB));
-  };
-  // Scores, online-softmax step and p*V accumulation for one loaded tile.
-  auto process_tile = [&](const Tile& t, int tb) {
-    f4_t c4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int u = 0; u < U; ++u) {
+      const uint32_t base = (uint32_t)(pb + u * step) * F::ROWB;
 #pragma unroll
-    for (int i = 0; i < F::NKI; ++i)
-      c4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[i], F::kfrag(t.kr, i), c4, 0, 0, 0);
-    const bool tok_ok = tb + kt < hi;
+      for (int j = 0; j < F::VLD; ++j) vr[u][j] = load_v<FMT, D>(rV, base + voff + (uint32_t)(j * F::TPL * F::ROWB));
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
+
+    f4_t c4[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      c4[u] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < F::NKI; ++i)
+        c4[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[i], F::kfrag(kr[u], i), c4[u], 0, 0, 0);
+    }
+
     float alpha[NR];
 #pragma unroll
     for (int rr = 0; rr < NR; ++rr) {
       const int h = kb + 4 * rr;
-      float x = c4[rr] * t.ksc;
-      x = (tok_ok && h < hcnt) ? x : -INFINITY;
-      const float mn = fmaxf(m_run[rr], row16_max(x));
+      const bool hv = h < hcnt;
+      float x[U];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool ok = hv && (pb + u * step + kt < hi);
+        x[u] = ok ? c4[u][rr] * ksc[u] : -INFINITY;
+        mx = fmaxf(mx, x[u]);
+      }
+      const float mn = fmaxf(m_run[rr], row16_max(mx));
       const float mu = (mn == -INFINITY) ? 0.0f : mn;
       alpha[rr] = fast_exp2((m_run[rr] - mu) * p.c);
-      const float pw = fast_exp2((x - mu) * p.c);
-      l_run[rr] = l_run[rr] * alpha[rr] + pw;
-      const float wv = pw * t.vsc;
-      if constexpr (F::QUANT) c_run[rr] = c_run[rr] * alpha[rr] + wv;
+      float psum = 0.0f, csum = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float pw = fast_exp2((x[u] - mu) * p.c);
+        const float wv = pw * vsc[u];
+        psum += pw;
+        csum += wv;
+        if (h < HG) s_w[w][u][kt][h] = wv;
+      }
+      l_run[rr] = l_run[rr] * alpha[rr] + psum;
+      if constexpr (F::QUANT) c_run[rr] = c_run[rr] * alpha[rr] + csum;
       m_run[rr] = mn;
-      if (h < HG) s_w[w][kt][h] = wv;
     }
     compiler_fence();
 #pragma unroll
@@ -326,37 +354,22 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       }
     }
 #pragma unroll
-    for (int j = 0; j < F::VLD; ++j) {
-      const int tl = j * F::TPL + vt;
-      float wt[HG];
+    for (int u = 0; u < U; ++u) {
 #pragma unroll
-      for (int h = 0; h < HG; ++h) wt[h] = s_w[w][tl][h];
-      float f[F::EV];
-      F::vconv(t.vr[j], f);
+      for (int j = 0; j < F::VLD; ++j) {
+        const int tl = j * F::TPL + vt;
+        float wt[HG];
 #pragma unroll
-      for (int h = 0; h < HG; ++h)
+        for (int h = 0; h < HG; ++h) wt[h] = s_w[w][u][tl][h];
+        float f[F::EV];
+        F::vconv(vr[u][j], f);
 #pragma unroll
-        for (int e = 0; e < F::EV; ++e) acc[h][e] = fmaf(wt[h], f[e], acc[h][e]);
+        for (int h = 0; h < HG; ++h)
+#pragma unroll
+          for (int e = 0; e < F::EV; ++e) acc[h][e] = fmaf(wt[h], f[e], acc[h][e]);
+      }
     }
     compiler_fence();
-  };
-
-  // Two-tile register pipeline: the next tile's loads are in flight while the
-  // current tile is processed. Every branch below is wave-uniform, and each
-  // path either prefetches before processing or processes the last tile, so
-  // the compiler's load counters wait only for the tile being consumed.
-  // Each pass a wave issues the loads of U tiles (interleaved with the other
-  // waves' tiles) before consuming any: straight-line code, so the load
-  // counter waits exactly for the tile about to be used while the rest of the
-  // pass is still in flight. Tiles past the split end are clamped and masked.
-  const int step = 16 * nw;
-  for (int pb = lo + 16 * w; pb < hi; pb += U * step) {
-    Tile t[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) load_tile(t[u], pb + u * step);
-    __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
-#pragma unroll
-    for (int u = 0; u < U; ++u) process_tile(t[u], pb + u * step);
   }
 
   // ---- wave totals ----
@@ -388,37 +401,30 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     for (int rr = 0; rr < NR; ++rr) {
       const int h = kb + 4 * rr;
       if (h < HG) {
-        s_m[w][h] = m_run[rr];
-        s_l[w][h] = l_run[rr];
+        s_m[h][w] = m_run[rr];
+        s_l[h][w] = l_run[rr];
       }
     }
   }
   __syncthreads();
 
   // ---- merge the waves, emit output or split scratch ----
-  // One thread per head first turns the waves' maxima into merge weights
-  // (an empty wave, m = -inf, gets weight 0; an all-empty split keeps M = -inf).
-  if (threadIdx.x < hcnt) {
-    const int h = threadIdx.x;
-    float M = -INFINITY;
-    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_m[ww][h]);
-    float L = 0.0f;
-    for (int ww = 0; ww < nw; ++ww) {
-      const float sc = (M == -INFINITY) ? 0.0f : fast_exp2((s_m[ww][h] - M) * p.c);
-      s_sc[ww][h] = sc;
-      L += sc * s_l[ww][h];
-    }
-    s_M[h] = M;
-    s_L[h] = L;
-  }
-  __syncthreads();
+  // Each (head, d) thread forms the waves' weights e^(m_w - M) itself from
+  // the head's LDS row (an empty wave, m = -inf, weighs 0; an empty split
+  // keeps M = -inf).
   for (int idx = threadIdx.x; idx < hcnt * D; idx += blockDim.x) {
     const int h = idx / D;
     const int d = idx - h * D;
-    const float M = s_M[h];
-    const float L = s_L[h];
-    float O = 0.0f;
-    for (int ww = 0; ww < nw; ++ww) O += s_sc[ww][h] * s_o[ww][h][d];
+    float M = -INFINITY;
+    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_m[h][ww]);
+    float L = 0.0f, O = 0.0f;
+    if (M != -INFINITY) {
+      for (int ww = 0; ww < nw; ++ww) {
+        const float sc = fast_exp2((s_m[h][ww] - M) * p.c);
+        L += sc * s_l[h][ww];
+        O += sc * s_o[ww][h][d];
+      }
+    }
     const size_t qh = qrow0 + h;
     if (p.direct) {
       p.o[qh * D + d] = (_Float16)(O / L);
