@@ -77,8 +77,8 @@ class HipEvents:
 
 
 def default_splits(cus):
-    # two workgroups (8 waves each) per CU across the 8 KV heads
-    return max(1, (2 * cus) // HKV)
+    # one 8-wave workgroup per CU across the 8 KV heads
+    return max(1, cus // HKV)
 
 
 def make_sets(torch, nsets, seed=0):
@@ -202,6 +202,8 @@ def main():
     ap.add_argument("--CW", type=int, default=8)
     ap.add_argument("--kv-sets", type=int, default=10, help="distinct 64 MiB KV caches cycled through")
     ap.add_argument("--sweep", action="store_true", help="tune S/W/CW first (table on stderr)")
+    ap.add_argument("--merge", choices=("fused", "two-kernel"), default="fused",
+                    help="split merge inside the partial kernel (default) or a separate combine kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration under rocprofv3 --pmc)")
@@ -217,6 +219,7 @@ def main():
     import fqkv_decode as fq
 
     cus = fq.cu_count()
+    fq._ext._set_two_kernel_merge(1 if args.merge == "two-kernel" else 0)
     if args.calib_copy_mib:
         n = args.calib_copy_mib << 20
         src = torch.ones(n, dtype=torch.uint8, device="cuda")
@@ -274,7 +277,7 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "gqa_sk_fast fp16 decode, Hq=32, Hkv=8, N=16384, D=128, batch 1",
-            "S": S, "W": W, "CW": CW,
+            "S": S, "W": W, "CW": CW, "merge": args.merge,
             "kv_sets": args.kv_sets,
             "kv_bytes_cycled": args.kv_sets * 4 * HKV * N * D,
             "alg_bytes_per_call": alg_bytes(),
@@ -283,7 +286,8 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_partial_kernel<fp16, D=128, HG=4>",
+            "kernel": "decode_partial_kernel<fp16, D=128, HG=4>"
+                      + (" (split merge fused in)" if args.merge == "fused" else ""),
             "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

@@ -10,15 +10,22 @@
 // split's last token, so rows past it read as zeros and need no clamping),
 // then consumes the tiles in order while the later ones are still arriving.
 // Per tile a wave
-//   1. has loaded the K tile as matrix-core operand B (dwordx4, 64 contiguous
-//      bytes per row per instruction) and the V tile as 16-byte row slices,
-//   2. computes all HG x 16 scores with D/32 v_mfma_f32_16x16x32_f16 (query
-//      head slots on the M axis, tokens on N),
-//   3. runs one online-softmax step per 16-lane row (= one head) with DPP
-//      row reductions and v_exp_f32 (exp(x) = 2^(x log2 e), log2 e folded
-//      into the score scale),
-//   4. hands the per-token weights to the V lanes through a wave-private LDS
-//      slot and accumulates p * V in fp32 registers.
+//   1. has loaded the K tile as matrix-core operand A (lane l: token l % 16,
+//      64 contiguous bytes of 16 rows per dwordx4 instruction) and the V tile
+//      as four loads of 4 whole rows each,
+//   2. computes the transposed scores S^T = K Q^T (tokens on M, query heads
+//      on N) with D/32 v_mfma_f32_16x16x32_f16, so lane l holds head l % 16
+//      for tokens 4 (l / 16) .. + 3,
+//   3. runs one online-softmax step per pass with v_exp_f32 (exp(x) =
+//      2^(x log2 e), log2 e folded into the score scale) and an all-reduce
+//      over the four lane rows; the weights p (times the per-token V scale
+//      for int8/int4), as fp16 pairs hi + lo, are then already in operand-B
+//      layout of
+//   4. O^T += V^T P^T with D/16 v_mfma_f32_16x16x16_f16, after a 4 x 4
+//      exchange of the V chunks between lane rows and registers
+//      (v_permlane32_swap / v_permlane16_swap) puts four tokens of one
+//      head-dim element in each operand slot; int8/int4 become exact fp16 on
+//      the way.
 // Waves of a workgroup take interleaved tiles; their (m, l, acc) states are
 // merged through LDS. With one split the workgroup writes the normalised
 // fp16 output; otherwise it writes the reference's fp32 scratch layout
@@ -40,50 +47,55 @@ namespace fqkv {
 
 constexpr float LOG2E = 1.4426950408889634f;
 
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
-}
-// All-reduce over each 16-lane row: quad_perm [1,0,3,2], quad_perm [2,3,0,1],
-// row_half_mirror, row_mirror.
-__device__ __forceinline__ float row16_max(float x) {
-  x = fmaxf(x, dpp<0xB1>(x));
-  x = fmaxf(x, dpp<0x4E>(x));
-  x = fmaxf(x, dpp<0x141>(x));
-  x = fmaxf(x, dpp<0x140>(x));
-  return x;
-}
-__device__ __forceinline__ float row16_sum(float x) {
-  x += dpp<0xB1>(x);
-  x += dpp<0x4E>(x);
-  x += dpp<0x141>(x);
-  x += dpp<0x140>(x);
-  return x;
-}
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-// Sum of x over the lanes of the wave that share (lane % LPR): rotations
-// within each 16-lane row for LPR < 16, then v_permlane16_swap (rows 0+1,
-// 2+3) and v_permlane32_swap (halves). Adding both swap outputs makes the
-// result independent of which operand receives which half. All VALU.
-template <int LPR>
-__device__ __forceinline__ float sum_over_token_rows(float x) {
-  if constexpr (LPR <= 4) x += dpp<0x124>(x);  // row_ror:4
-  if constexpr (LPR <= 8) x += dpp<0x128>(x);  // row_ror:8
-  // (swap results are copied to scalars before the bit casts: this
-  // compiler's __builtin_bit_cast of a vector element reads element 0)
-  const unsigned u = __builtin_bit_cast(unsigned, x);
-  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  const unsigned a = r16[0], b = r16[1];
+
+// Row exchanges between the four 16-lane rows of a wave (all VALU):
+// v_permlane32_swap trades rows 2,3 of its first operand for rows 0,1 of its
+// second; v_permlane16_swap trades the odd rows of its first operand for the
+// even rows of its second. The builtins return {first, second} after the
+// trade (copied to scalars: this compiler's __builtin_bit_cast of a
+// vector-element expression reads element 0 whatever the index).
+__device__ __forceinline__ void swap_rows32(uint32_t& a, uint32_t& b) {
+  const auto t = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  const uint32_t x = t[0], y = t[1];
+  a = x;
+  b = y;
+}
+__device__ __forceinline__ void swap_rows16(uint32_t& a, uint32_t& b) {
+  const auto t = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  const uint32_t x = t[0], y = t[1];
+  a = x;
+  b = y;
+}
+// 4 x 4 exchange between lane rows and registers: afterwards row R of
+// register j holds what row j of register R held.
+__device__ __forceinline__ void exchange_4x4(uint32_t& a0, uint32_t& a1, uint32_t& a2, uint32_t& a3) {
+  swap_rows32(a0, a2);
+  swap_rows32(a1, a3);
+  swap_rows16(a0, a1);
+  swap_rows16(a2, a3);
+}
+// All-reduce over the four lane rows (lanes with equal lane % 16). Combining
+// both outputs of each swap makes the result independent of which operand
+// receives which rows.
+__device__ __forceinline__ float rows4_max(float x) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+  swap_rows32(a, b);
+  x = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  a = __builtin_bit_cast(uint32_t, x);
+  b = a;
+  swap_rows16(a, b);
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+__device__ __forceinline__ float rows4_sum(float x) {
+  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+  swap_rows32(a, b);
   x = __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
-  const unsigned v = __builtin_bit_cast(unsigned, x);
-  const auto r32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
-  const unsigned c = r32[0], d = r32[1];
-  return __builtin_bit_cast(float, c) + __builtin_bit_cast(float, d);
+  a = __builtin_bit_cast(uint32_t, x);
+  b = a;
+  swap_rows16(a, b);
+  return __builtin_bit_cast(float, a) + __builtin_bit_cast(float, b);
 }
-__device__ __forceinline__ float readlane_f(float x, int lane) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), lane));
-}
-__device__ __forceinline__ void compiler_fence() { __asm__ __volatile__("" ::: "memory"); }
 
 typedef float fl4_t __attribute__((ext_vector_type(4)));
 
@@ -203,13 +215,15 @@ __device__ void merge_splits(const float* __restrict__ m_part, const float* __re
 template <int FMT, int D, int HG>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
-  constexpr int U = 4;
-  constexpr int NR = (HG + 3) / 4;  // MFMA result registers that carry heads
-  __shared__ float s_w[NW_MAX][U][16][HG];
+  using VG = VGeom<F::ROWB, D>;
+  // tiles per pass (int8 at D = 128 converts more K per tile: three fit the registers)
+  constexpr int U = (FMT == KV_I8 && D == 128) ? 3 : 4;
+  constexpr int VE = VG::VE;   // PV steps per tile
+  constexpr int VD = VG::VD;   // dwords per V chunk
   __shared__ float s_o[NW_MAX][HG][D];
   __shared__ float s_m[HG][NW_MAX];
   __shared__ float s_l[HG][NW_MAX];
-  __shared__ fl4_t s_macc[64 * NW_MAX];        // in-kernel split merge
+  __shared__ fl4_t s_macc[64 * NW_MAX];  // in-kernel split merge
   __shared__ float s_mred[2 * 64 * NW_MAX / (D / 4)];
   __shared__ int s_last;
 
@@ -232,36 +246,23 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   const _Float16* Ksr = F::QUANT ? p.Ks + (size_t)r * p.N : nullptr;
   const _Float16* Vsr = F::QUANT ? p.Vs + (size_t)r * p.N : nullptr;
 
-  const int kt = lane & 15;  // token of the tile this lane scores
-  const int kb = lane >> 4;  // K dword group / head-slot group
-  const int vl = lane % F::LPR;
-  const int vt = lane / F::LPR;
+  const int n = lane & 15;  // query head column of P^T and O^T; token row of the K operand
+  const int R = lane >> 4;  // lane row: K dword group; scores and V of tokens 4R .. 4R+3
 
-  // Query fragment (MFMA operand A). Row m = lane % 16 carries head slot
-  // 4 (m % 4) + m / 4, so result register rr of lane l holds head (l / 16) + 4 rr.
-  // The descriptor covers only this group's hcnt query rows: slots past them
-  // read as zeros and score nothing.
-  h8_t qa[F::NKI];
+  // Query operand B of the score product: lane l holds head n, elements
+  // kd_index(i, R, 0..7). The descriptor covers only this group's hcnt query
+  // rows; head columns past them read zeros and are never emitted.
+  h8_t qb[F::NKI];
   {
-    const int m = lane & 15;
-    const int h = 4 * (m & 3) + (m >> 2);
     const rsrc_t rQ = make_rsrc(p.q + qrow0 * D, (uint32_t)hcnt * D * 2);
 #pragma unroll
-    for (int i = 0; i < F::NKI; ++i) qa[i] = F::qfrag(rQ, (uint32_t)h * D, i, kb);
+    for (int i = 0; i < F::NKI; ++i) qb[i] = F::qfrag(rQ, (uint32_t)n * D, i, R);
   }
 
-  float m_run[NR], l_run[NR], c_run[NR];
+  float m_run = -INFINITY, l_run = 0.0f;  // of head n, over the tokens this lane scored
+  f4_t acc[VE];                           // O^T: step c, reg k = head-dim VE (4R + k) + c of head n
 #pragma unroll
-  for (int rr = 0; rr < NR; ++rr) {
-    m_run[rr] = -INFINITY;
-    l_run[rr] = 0.0f;
-    c_run[rr] = 0.0f;
-  }
-  float acc[HG][F::EV];
-#pragma unroll
-  for (int h = 0; h < HG; ++h)
-#pragma unroll
-    for (int e = 0; e < F::EV; ++e) acc[h][e] = 0.0f;
+  for (int c = 0; c < VE; ++c) acc[c] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // Buffer descriptors end at the split's last token, so rows past it read
   // as zeros (their scores are masked); offsets are 32-bit from the row block.
@@ -270,39 +271,43 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   const rsrc_t rV = make_rsrc(Vr, nbytes);
   const rsrc_t rKs = make_rsrc(Ksr, 2u * (uint32_t)hi);
   const rsrc_t rVs = make_rsrc(Vsr, 2u * (uint32_t)hi);
-  const uint32_t koff = (uint32_t)kt * F::ROWB + F::klane(kb);
-  const uint32_t voff = (uint32_t)vt * F::ROWB + (uint32_t)vl * F::VB;
+  const uint32_t koff = (uint32_t)n * F::ROWB + F::klane(R);
+  const uint32_t voff = (uint32_t)R * F::ROWB + (uint32_t)n * VG::VBYTES;
 
   // Each pass covers U tiles of this wave (tiles interleave across waves).
   // All K loads of the pass are issued, then all V loads, before anything is
   // consumed: straight-line code, so the load counter waits exactly for the
-  // data about to be used while the rest is still arriving. The pass then
-  // scores all U tiles with the matrix cores, takes ONE online-softmax step
-  // over its 16 U tokens per row (one max reduction, one rescale), and
-  // accumulates p * V.
+  // data about to be used while the rest is still arriving. The pass scores
+  // its U tiles with the matrix cores (S^T: tokens on M, heads on N), takes
+  // ONE online-softmax step over its 16 U tokens per head, and accumulates
+  // O^T += V^T P^T on the matrix cores: the score result layout (lane: head
+  // n, tokens 4R + k) is exactly operand B of the PV product.
   const int step = 16 * nw;
   for (int pb = lo + 16 * w; pb < hi; pb += U * step) {
     typename F::KT kr[U][F::KL];
-    vraw_t<F::VB> vr[U][F::VLD];
-    float ksc[U], vsc[U];
+    uint32_t vr[U][4][VD];
+    _Float16 ks[U][4], vs[U][4];  // per-token scales of tokens 4R + k (int8 / int4)
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t base = (uint32_t)(pb + u * step) * F::ROWB;
-      F::load_k(rK, base + koff, kr[u]);
-      if constexpr (F::QUANT) {
-        const uint32_t so = 2u * (uint32_t)(pb + u * step + kt);
-        ksc[u] = (float)__builtin_bit_cast(_Float16, buf_load<2>(rKs, so));
-        vsc[u] = (float)__builtin_bit_cast(_Float16, buf_load<2>(rVs, so));
-      } else {
-        ksc[u] = 1.0f;
-        vsc[u] = 1.0f;
+      const int tb = pb + u * step;
+      F::load_k(rK, (uint32_t)tb * F::ROWB + koff, kr[u]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (F::QUANT) {
+          const uint32_t so = 2u * (uint32_t)(tb + 4 * R + k);
+          ks[u][k] = __builtin_bit_cast(_Float16, buf_load<2>(rKs, so));
+          vs[u][k] = __builtin_bit_cast(_Float16, buf_load<2>(rVs, so));
+        } else {
+          ks[u][k] = (_Float16)1.0f;
+          vs[u][k] = (_Float16)1.0f;
+        }
       }
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t base = (uint32_t)(pb + u * step) * F::ROWB;
+      const uint32_t base = (uint32_t)(pb + u * step) * F::ROWB + voff;
 #pragma unroll
-      for (int j = 0; j < F::VLD; ++j) vr[u][j] = load_v<FMT, D>(rV, base + voff + (uint32_t)(j * F::TPL * F::ROWB));
+      for (int j = 0; j < 4; ++j) load_vchunk<VG::VBYTES, VD>(rV, base + (uint32_t)(4 * j) * F::ROWB, vr[u][j]);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
 
@@ -312,98 +317,70 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       c4[u] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < F::NKI; ++i)
-        c4[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[i], F::kfrag(kr[u], i), c4[u], 0, 0, 0);
+        c4[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(F::kfrag(kr[u], i), qb[i], c4[u], 0, 0, 0);
     }
 
-    float alpha[NR];
+    float x[U][4];
+    float mx = -INFINITY;
 #pragma unroll
-    for (int rr = 0; rr < NR; ++rr) {
-      const int h = kb + 4 * rr;
-      const bool hv = h < hcnt;
-      float x[U];
-      float mx = -INFINITY;
+    for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const bool ok = hv && (pb + u * step + kt < hi);
-        x[u] = ok ? c4[u][rr] * ksc[u] : -INFINITY;
-        mx = fmaxf(mx, x[u]);
+      for (int k = 0; k < 4; ++k) {
+        const bool ok = pb + u * step + 4 * R + k < hi;
+        x[u][k] = ok ? c4[u][k] * (float)ks[u][k] : -INFINITY;
+        mx = fmaxf(mx, x[u][k]);
       }
-      const float mn = fmaxf(m_run[rr], row16_max(mx));
-      const float mu = (mn == -INFINITY) ? 0.0f : mn;
-      alpha[rr] = fast_exp2((m_run[rr] - mu) * p.c);
-      float psum = 0.0f, csum = 0.0f;
+    const float mn = fmaxf(m_run, rows4_max(mx));
+    const float mu = (mn == -INFINITY) ? 0.0f : mn;
+    const float alpha = fast_exp2((m_run - mu) * p.c);
+    // The PV operand carries each fp32 weight as an fp16 pair hi + lo
+    // (hi = fp16(w), lo = fp16(w - hi)): two matrix-core steps reproduce the
+    // fp32 weight to ~2^-22 relative, V being exact in fp16.
+    h4_t phi[U], plo[U];
+    float psum = 0.0f;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const float pw = fast_exp2((x[u] - mu) * p.c);
-        const float wv = pw * vsc[u];
+    for (int u = 0; u < U; ++u)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float pw = fast_exp2((x[u][k] - mu) * p.c);
         psum += pw;
-        csum += wv;
-        if (h < HG) s_w[w][u][kt][h] = wv;
+        const float wv = pw * (float)vs[u][k];
+        const _Float16 h = (_Float16)wv;
+        phi[u][k] = h;
+        plo[u][k] = (_Float16)(wv - (float)h);
       }
-      l_run[rr] = l_run[rr] * alpha[rr] + psum;
-      if constexpr (F::QUANT) c_run[rr] = c_run[rr] * alpha[rr] + csum;
-      m_run[rr] = mn;
-    }
-    compiler_fence();
+    l_run = l_run * alpha + psum;
+    m_run = mn;
 #pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      const float a = readlane_f(alpha[h / 4], 16 * (h % 4));
-      if (a != 1.0f) {
-#pragma unroll
-        for (int e = 0; e < F::EV; ++e) acc[h][e] *= a;
-      }
-    }
+    for (int c = 0; c < VE; ++c) acc[c] *= alpha;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
-      for (int j = 0; j < F::VLD; ++j) {
-        const int tl = j * F::TPL + vt;
-        float wt[HG];
+      for (int dw = 0; dw < VD; ++dw) exchange_4x4(vr[u][0][dw], vr[u][1][dw], vr[u][2][dw], vr[u][3][dw]);
+      h4_t vf[VE];
 #pragma unroll
-        for (int h = 0; h < HG; ++h) wt[h] = s_w[w][u][tl][h];
-        float f[F::EV];
-        F::vconv(vr[u][j], f);
-#pragma unroll
-        for (int h = 0; h < HG; ++h)
-#pragma unroll
-          for (int e = 0; e < F::EV; ++e) acc[h][e] = fmaf(wt[h], f[e], acc[h][e]);
+      for (int c = 0; c < VE; ++c) {
+        vf[c] = vfrag<FMT, D>(vr[u], c);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[c], phi[u], acc[c], 0, 0, 0);
       }
+#pragma unroll
+      for (int c = 0; c < VE; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[c], plo[u], acc[c], 0, 0, 0);
     }
-    compiler_fence();
   }
 
-  // ---- wave totals ----
+  // ---- wave totals: l over the four lane rows; O^T rows are disjoint ----
+  l_run = rows4_sum(l_run);
+  if (n < HG && n < hcnt) {
 #pragma unroll
-  for (int rr = 0; rr < NR; ++rr) {
-    l_run[rr] = row16_sum(l_run[rr]);
-    if constexpr (F::QUANT) c_run[rr] = row16_sum(c_run[rr]);
-  }
+    for (int k = 0; k < 4; ++k) {
+      float* dst = &s_o[w][n][VE * (4 * R + k)];
 #pragma unroll
-  for (int h = 0; h < HG; ++h)
-#pragma unroll
-    for (int e = 0; e < F::EV; ++e) acc[h][e] = sum_over_token_rows<F::LPR>(acc[h][e]);
-  if constexpr (F::QUANT) {
-#pragma unroll
-    for (int h = 0; h < HG; ++h) {
-      const float cw = readlane_f(c_run[h / 4], 16 * (h % 4));
-#pragma unroll
-      for (int e = 0; e < F::EV; ++e) acc[h][e] -= F::VBIAS * cw;
+      for (int c = 0; c < VE; c += 4)
+        *reinterpret_cast<fl4_t*>(dst + c) = fl4_t{acc[c][k], acc[c + 1][k], acc[c + 2][k], acc[c + 3][k]};
     }
-  }
-  if (lane < F::LPR) {
-#pragma unroll
-    for (int h = 0; h < HG; ++h)
-#pragma unroll
-      for (int e = 0; e < F::EV; ++e) s_o[w][h][F::vd_index(lane, e)] = acc[h][e];
-  }
-  if (kt == 0) {
-#pragma unroll
-    for (int rr = 0; rr < NR; ++rr) {
-      const int h = kb + 4 * rr;
-      if (h < HG) {
-        s_m[h][w] = m_run[rr];
-        s_l[h][w] = l_run[rr];
-      }
+    if (R == 0) {
+      s_m[n][w] = m_run;
+      s_l[n][w] = l_run;
     }
   }
   __syncthreads();
@@ -411,18 +388,28 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // ---- merge the waves, emit output or split scratch ----
   // Each (head, d) thread forms the waves' weights e^(m_w - M) itself from
   // the head's LDS row (an empty wave, m = -inf, weighs 0; an empty split
-  // keeps M = -inf).
+  // keeps M = -inf). Unrolled over NW_MAX with selects, so the LDS reads of
+  // all waves are in flight together; slots of absent waves hold stale LDS
+  // and are selected, never multiplied, away.
   for (int idx = threadIdx.x; idx < hcnt * D; idx += blockDim.x) {
     const int h = idx / D;
     const int d = idx - h * D;
+    float mw[NW_MAX], lw[NW_MAX], ow[NW_MAX];
     float M = -INFINITY;
-    for (int ww = 0; ww < nw; ++ww) M = fmaxf(M, s_m[h][ww]);
+#pragma unroll
+    for (int ww = 0; ww < NW_MAX; ++ww) {
+      mw[ww] = s_m[h][ww];
+      lw[ww] = s_l[h][ww];
+      ow[ww] = s_o[ww][h][d];
+      if (ww < nw) M = fmaxf(M, mw[ww]);
+    }
     float L = 0.0f, O = 0.0f;
     if (M != -INFINITY) {
-      for (int ww = 0; ww < nw; ++ww) {
-        const float sc = fast_exp2((s_m[h][ww] - M) * p.c);
-        L += sc * s_l[h][ww];
-        O += sc * s_o[ww][h][d];
+#pragma unroll
+      for (int ww = 0; ww < NW_MAX; ++ww) {
+        const float sc = fast_exp2((mw[ww] - M) * p.c);
+        L += (ww < nw) ? sc * lw[ww] : 0.0f;
+        O += (ww < nw) ? sc * ow[ww] : 0.0f;
       }
     }
     const size_t qh = qrow0 + h;
@@ -503,14 +490,18 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
       for (int e = 0; e < 8; ++e) out[t * D + F::kd_index(i, kb, e)] = (float)b[e] * sc;
     }
   } else {
-    const int64_t t = g / F::LPR;
-    const int lir = (int)(g % F::LPR);
+    using VG = VGeom<F::ROWB, D>;
+    const int64_t t = g / 16;
+    const int i = (int)(g % 16);
     if (t >= tokens) return;
-    float f[F::EV];
-    F::vconv(load_v<FMT, D>(make_rsrc(Kq + t * F::ROWB, F::ROWB), (uint32_t)lir * F::VB), f);
+    uint32_t d[VG::VD];
+    load_vchunk<VG::VBYTES, VG::VD>(make_rsrc(Kq + t * F::ROWB, F::ROWB), (uint32_t)i * VG::VBYTES, d);
     const float sc = (float)Ks[t];
 #pragma unroll
-    for (int e = 0; e < F::EV; ++e) out[t * D + F::vd_index(lir, e)] = (f[e] - F::VBIAS) * sc;
+    for (int c = 0; c < VG::VE; ++c) {
+      const h2_t h = F::vpair(d[c / VG::EPD], d[c / VG::EPD], c % VG::EPD);
+      out[t * D + VG::VE * i + c] = (float)h.x * sc;
+    }
   }
 }
 
@@ -529,6 +520,7 @@ static hipError_t launch_partial_d(int hg, const PartialParams& p, int nblocks, 
       case 2: return launch_partial_t<FMT, D, 2>(p, nblocks, nw, st);
       case 4: return launch_partial_t<FMT, D, 4>(p, nblocks, nw, st);
       case 8: return launch_partial_t<FMT, D, 8>(p, nblocks, nw, st);
+      case 16: return launch_partial_t<FMT, D, 16>(p, nblocks, nw, st);
     }
   } else {
     if (hg == 1) return launch_partial_t<FMT, D, 1>(p, nblocks, nw, st);
@@ -564,9 +556,8 @@ hipError_t launch_combine(int D, const float* m_part, const float* l_part, const
 
 hipError_t launch_dequant(int fmt, int D, int path, const void* Kq, const void* Ks, float* out,
                           int64_t tokens, hipStream_t st) {
-  const int lpr = (fmt == KV_I8) ? (D == 128 ? Fmt<KV_I8, 128>::LPR : Fmt<KV_I8, 64>::LPR)
-                                 : (D == 128 ? Fmt<KV_I4, 128>::LPR : Fmt<KV_I4, 64>::LPR);
-  const int64_t threads = tokens * (path == 0 ? 4 : lpr);
+  // path 0: one thread per (token, K lane group); path 1: per (token, V chunk)
+  const int64_t threads = tokens * (path == 0 ? 4 : 16);
   const int64_t blocks = (threads + 255) / 256;
   const auto* k = (const uint8_t*)Kq;
   const auto* s = (const _Float16*)Ks;

@@ -1,20 +1,27 @@
 // KV-cache formats as seen by the gfx950 decode kernels.
 //
-// One 16-token tile of a KV row block is consumed two ways:
-//   * K side: operand B of v_mfma_f32_16x16x32_f16. Lane l holds token
-//     (l % 16) of the tile and 8 head-dim elements per MFMA step for lane
-//     group kb = l / 16. Which head-dim element sits in which operand slot
-//     is free (the contraction sums over all of them) as long as the query
-//     fragment (operand A) uses the same map, kd_index(). Each format picks
-//     the map that keeps its global loads wide and contiguous and its
-//     int -> fp16 conversion cheap.
-//   * V side: plain VALU. A token row is split over LPR lanes, each holding
-//     VB contiguous bytes = EV elements; a wave covers TPL tokens per load.
+// A wave consumes a 16-token tile of a KV row block with two matrix-core
+// products, scores first and then P.V, both with the token index where the
+// hardware wants it without any data shuffling through LDS:
+//   * K side: operand A of v_mfma_f32_16x16x32_f16 (scores transposed,
+//     S^T = K Q^T). Lane l holds token (l % 16) of the tile and 8 head-dim
+//     elements per MFMA step for lane group kb = l / 16. Which head-dim
+//     element sits in which operand slot is free (the contraction sums over
+//     all of them) as long as the query fragment (operand B) uses the same
+//     map, kd_index(). Each format picks the map that keeps its global loads
+//     wide and its int -> fp16 conversion cheap.
+//   * V side: operand A of v_mfma_f32_16x16x16_f16 (O^T += V^T P^T). Lane
+//     (R = l / 16, i = l % 16) loads VBYTES = ROWB / 16 contiguous bytes at
+//     byte VBYTES * i of tile row 4 j + R (j = 0..3: four loads per tile,
+//     each covering 4 whole rows). A 4 x 4 exchange of those chunks between
+//     lane rows and loads (v_permlane32_swap, v_permlane16_swap) leaves lane
+//     (R, i) with tokens 4 R .. 4 R + 3 of head-dim elements VE * i .. + VE-1,
+//     and element c of the four chunks is the lane's operand of PV step c
+//     (VE = D / 16 steps per tile).
 //
 // Exactness: int8 and int4 values become fp16 through the 0x6400 exponent
 // trick (1024 + u is exact in fp16 for 0 <= u < 1024) followed by an exact
-// subtraction, and become fp32 through v_cvt_f32_ubyte; both are exact, so
-// the dequantised value (float)q * (float)scale
+// subtraction, so the dequantised value (float)q * (float)scale
 // (decode_attn_int8_mw.cu:24,31; decode_attn_int4.cu:21-23,29-31) is
 // reproduced bit for bit by fqkv_dequant_kv, which calls these same helpers.
 #pragma once
@@ -27,6 +34,7 @@
 namespace fqkv {
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
@@ -64,14 +72,11 @@ __device__ __forceinline__ void i4x8_to_h2x4(uint32_t w, h2_t (&h)[4]) {
   h[3] = bytes_under_1024(hi, SEL_B23) - off;
 }
 
-__device__ __forceinline__ float ubyte_f(uint32_t w, int k) {
-  return (float)((w >> (8 * k)) & 0xFFu);  // v_cvt_f32_ubyte{k}
-}
-
 // Raw buffer access (gfx9 descriptor word 3 = 0x00020000, stride 0):
 // loads whose byte offset is at or past num_records return zeros.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int CPOL_SC1 = 16;  // cache-policy bit: device-scope coherent access
+constexpr int CPOL_NT = 2;    // cache-policy bit: non-temporal (streaming) access
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
@@ -81,10 +86,41 @@ __device__ __forceinline__ auto buf_load(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
   } else if constexpr (BYTES == 8) {
     return __builtin_bit_cast(u2_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+  } else if constexpr (BYTES == 4) {
+    return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
   } else {
     return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
   }
 }
+
+// V chunk of VBYTES bytes as VD dwords (a 2-byte chunk is zero-extended).
+// V rows are read whole by one instruction stream and never again: the loads
+// carry the non-temporal hint.
+template <int VBYTES, int VD>
+__device__ __forceinline__ void load_vchunk(rsrc_t r, uint32_t off, uint32_t (&d)[VD]) {
+  if constexpr (VBYTES == 16) {
+    const u4_t v = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CPOL_NT));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) d[k] = v[k];
+  } else if constexpr (VBYTES == 8) {
+    const u2_t v = __builtin_bit_cast(u2_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, CPOL_NT));
+    d[0] = v[0];
+    d[1] = v[1];
+  } else if constexpr (VBYTES == 4) {
+    d[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, CPOL_NT);
+  } else {
+    d[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, CPOL_NT);
+  }
+}
+
+// Common V-side geometry (ROWB bytes per token row, D head-dim elements).
+template <int ROWB_, int D_>
+struct VGeom {
+  static constexpr int VBYTES = ROWB_ / 16;                 // bytes per lane per load
+  static constexpr int VD = VBYTES >= 4 ? VBYTES / 4 : 1;   // dwords per lane per load
+  static constexpr int VE = D_ / 16;                        // elements per chunk = PV steps
+  static constexpr int EPD = (D_ / 16 + VD - 1) / VD;        // elements per dword
+};
 
 template <int FMT, int D>
 struct Fmt;
@@ -112,24 +148,10 @@ struct Fmt<KV_F16, D> {
   __device__ static h8_t qfrag(rsrc_t rq, uint32_t row_elem, int i, int kb) {
     return __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
   }
-  static constexpr int VB = 16;              // bytes per lane per V load
-  static constexpr int LPR = ROWB / VB;      // lanes per token row
-  static constexpr int TPL = 64 / LPR;       // tokens per wave load
-  static constexpr int VLD = 16 / TPL;       // V loads per tile
-  static constexpr int EV = 8;               // elements per lane per V load
-  static constexpr float VBIAS = 0.0f;
-  __device__ static void vconv(const u4_t vd, float (&f)[EV]) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      // element copied to a scalar first: this compiler's __builtin_bit_cast of
-      // a vector-element expression reads element 0 whatever the index
-      const uint32_t x = vd[k];
-      const h2_t h = __builtin_bit_cast(h2_t, x);
-      f[2 * k] = (float)h.x;
-      f[2 * k + 1] = (float)h.y;
-    }
+  // element pos (0, 1) of dwords a and b -> half2 (a_pos, b_pos)
+  __device__ static h2_t vpair(uint32_t a, uint32_t b, int pos) {
+    return __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(b, a, pos ? 0x07060302u : 0x05040100u));
   }
-  __host__ __device__ static constexpr int vd_index(int lir, int e) { return EV * lir + e; }
 };
 
 // ---------------------------------------------------------------- int8 ----
@@ -159,21 +181,15 @@ struct Fmt<KV_I8, D> {
   __device__ static h8_t qfrag(rsrc_t rq, uint32_t row_elem, int i, int kb) {
     return __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
   }
-  static constexpr int VB = 16;
-  static constexpr int LPR = ROWB / VB;
-  static constexpr int TPL = 64 / LPR;
-  static constexpr int VLD = 16 / TPL;
-  static constexpr int EV = 16;
-  static constexpr float VBIAS = 128.0f;  // vconv yields x + 128
-  __device__ static void vconv(const u4_t vd, float (&f)[EV]) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t t = vd[k] ^ 0x80808080u;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) f[4 * k + b] = ubyte_f(t, b);
-    }
+  // byte pos of dwords a and b -> exact half2 (a_pos, b_pos): the bytes are
+  // placed in the low byte of each half, x ^ 0x80 = x + 128 is put under the
+  // 0x64 exponent byte (1024 + x + 128) and 1152 is subtracted.
+  __device__ static h2_t vpair(uint32_t a, uint32_t b, int pos) {
+    const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + pos) << 16) | (uint32_t)pos;
+    const uint32_t t = __builtin_amdgcn_perm(b, a, sel) ^ 0x64806480u;
+    const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    return __builtin_bit_cast(h2_t, t) - off;
   }
-  __host__ __device__ static constexpr int vd_index(int lir, int e) { return EV * lir + e; }
 };
 
 // ---------------------------------------------------------------- int4 ----
@@ -203,35 +219,31 @@ struct Fmt<KV_I4, D> {
     const h8_t v = __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
     return h8_t{v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]};
   }
-  static constexpr int VB = (D == 128) ? 16 : 8;
-  static constexpr int LPR = ROWB / VB;  // 4
-  static constexpr int TPL = 64 / LPR;   // 16
-  static constexpr int VLD = 16 / TPL;   // 1
-  static constexpr int EV = 2 * VB;
-  static constexpr float VBIAS = 8.0f;   // vconv yields n + 8
-  template <typename VT>
-  __device__ static void vconv(const VT vd, float (&f)[EV]) {
-#pragma unroll
-    for (int k = 0; k < VB / 4; ++k) {
-      const uint32_t t = vd[k] ^ 0x88888888u;
-      const uint32_t lo = t & 0x0F0F0F0Fu;
-      const uint32_t hi = (t >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        f[8 * k + 2 * b] = ubyte_f(lo, b);
-        f[8 * k + 2 * b + 1] = ubyte_f(hi, b);
-      }
-    }
+  // nibble pos (element pos; byte pos / 2, low nibble first) of dwords a and
+  // b -> exact half2 (a_pos, b_pos): n ^ 8 = n + 8 (mod 16) under the 0x64
+  // exponent byte (1024 + n + 8), then 1032 is subtracted.
+  __device__ static h2_t vpair(uint32_t a, uint32_t b, int pos) {
+    const uint32_t byte = (uint32_t)(pos >> 1);
+    const uint32_t sel = 0x0C000C00u | ((4u + byte) << 16) | byte;
+    uint32_t t = __builtin_amdgcn_perm(b, a, sel);
+    if (pos & 1) t >>= 4;
+    t = (t & 0x000F000Fu) ^ 0x64086408u;
+    const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
+    return __builtin_bit_cast(h2_t, t) - off;
   }
-  __host__ __device__ static constexpr int vd_index(int lir, int e) { return EV * lir + e; }
 };
 
-template <int VB>
-using vraw_t = typename std::conditional<VB == 16, u4_t, u2_t>::type;
-
+// V-side operand of PV step c from the four exchanged chunks of a tile (lane
+// (R, i) chunk j = token 4 R + j): slot k of the half4 = token 4 R + k,
+// head-dim element VE * i + c.
 template <int FMT, int D>
-__device__ __forceinline__ vraw_t<Fmt<FMT, D>::VB> load_v(rsrc_t r, uint32_t off) {
-  return buf_load<Fmt<FMT, D>::VB>(r, off);
+__device__ __forceinline__ h4_t vfrag(const uint32_t (&v)[4][VGeom<Fmt<FMT, D>::ROWB, D>::VD], int c) {
+  using G = VGeom<Fmt<FMT, D>::ROWB, D>;
+  const int dw = c / G::EPD;
+  const int pos = c % G::EPD;
+  const h2_t lo = Fmt<FMT, D>::vpair(v[0][dw], v[1][dw], pos);
+  const h2_t hi = Fmt<FMT, D>::vpair(v[2][dw], v[3][dw], pos);
+  return h4_t{lo.x, lo.y, hi.x, hi.y};
 }
 
 }  // namespace fqkv
