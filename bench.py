@@ -11,12 +11,17 @@ before timing starts.
 Reported: ``value`` = algorithmic bytes per call / time per call in GB/s
 (bytes = 4*Hkv*N*D (K+V fp16) + 4*Hq*D (q in, o out), i.e. 67,125,248),
 whole-call loop timing like the reference's flashinfer_looptimed.py:34-44.
-``roofline`` covers the dominant (partial) kernel, timed per launch with HIP
-events recorded around it on its own stream. ``cpu_baseline`` times the
-numpy oracle on the host for a bounded sample of the same workload.
+``roofline`` covers the dominant kernel. By default a call is ONE kernel
+(partial kernel with the split merge fused in), so its average duration is
+the loop time per call, taken with HIP events on the stream the kernel runs
+on (PyTorch's current stream). With --merge two-kernel the partial kernel is
+timed per launch with HIP events recorded just around it. ``cpu_baseline``
+times the numpy oracle on the host for a bounded sample of the same workload.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--S S --W W --CW CW]
        python bench.py --sweep      (tuning table on stderr, then the JSON line)
+       python bench.py --suite FILE (secondary configurations as JSON lines in
+                                     FILE and a table on stderr, then the JSON line)
 """
 
 import argparse
@@ -147,7 +152,7 @@ def time_partial(torch, fq, q, Ks, Vs, S, W, CW, steps, ev):
 
 def read_traffic():
     """HBM bytes per partial launch from the committed rocprofv3 PMC summary, if present."""
-    path = os.path.join(ROOT, "profiles", "gqa_sk_partial_n16k_d128_pmc.md")
+    path = os.path.join(ROOT, "profiles", "decode_partial_gqa_n16k_d128_pmc.md")
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -192,6 +197,209 @@ def cpu_baseline(budget_s=15.0):
     }
 
 
+# ---------------------------------------------------------------------------
+# Secondary configurations (the reference's other benchmarks, on MI355X).
+# Each is loop-timed like the headline: warm-up, then `steps` calls between
+# HIP events on the current stream, cycling through enough distinct input sets
+# that >= 1 GiB of KV streams per cycle (the 256 MB Infinity Cache cannot hold
+# it). Algorithmic bytes count compact K/V, scales, q and o only.
+
+def _nsets(bytes_per_set, cap=64):
+    return max(1, min(cap, -(-(1 << 30) // bytes_per_set)))
+
+
+def _loop_ms(torch, fn, nsets, steps, warmup):
+    for i in range(warmup):
+        fn(i % nsets)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        fn(i % nsets)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def _row(name, cfg, ms, nbytes, err=None, **extra):
+    r = {"bench": name, "config": cfg, "us_per_call": round(ms * 1e3, 3),
+         "alg_bytes": nbytes, "GBps": round(nbytes / ms / 1e6, 1),
+         "frac_of_8TBps": round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4)}
+    if err is not None:
+        r["max_abs_err_vs_fp32"] = err
+    r.update(extra)
+    return r
+
+
+def _ref_mha(torch, q, Kf, Vf):
+    """fp32 softmax(q K^T / sqrt(D)) V on the GPU, q [B, D], K/V [B, N, D] fp32."""
+    D = q.shape[-1]
+    s = torch.bmm(Kf, q.float().unsqueeze(2)).squeeze(2) / math.sqrt(D)
+    return torch.bmm(torch.softmax(s, dim=1).unsqueeze(1), Vf).squeeze(1)
+
+
+def suite_mha_quant(torch, fq, steps, warmup, rows):
+    """fp16 / int8 / int4 MHA decode at B in {8, 256, 2048}, N=4096, D=128, W=8."""
+    from fqkv_decode import quant
+    N, Dm, W = 4096, 128, 8
+    for B in (8, 256, 2048):
+        g = torch.Generator(device="cuda").manual_seed(1)
+        q = torch.randn(B, Dm, device="cuda", generator=g).half()
+        per = {"fp16": 2 * B * N * Dm * 2, "int8": 2 * B * N * Dm + 4 * B * N, "int4": B * N * Dm + 4 * B * N}
+        for fmt in ("fp16", "int8", "int4"):
+            ns = _nsets(per[fmt])
+            sets = []
+            err = None
+            for k in range(ns):
+                Kx = torch.randn(B, N, Dm, device="cuda", generator=g)
+                Vx = torch.randn(B, N, Dm, device="cuda", generator=g)
+                if fmt == "fp16":
+                    Kh, Vh = Kx.half(), Vx.half()
+                    sets.append((Kh, Vh))
+                    if k == 0:
+                        Kf, Vf = Kh.float(), Vh.float()
+                elif fmt == "int8":
+                    Kq, Ks = quant.quant_int8_per_token(Kx)
+                    Vq, Vs = quant.quant_int8_per_token(Vx)
+                    sets.append((Kq, Vq, Ks, Vs))
+                    if k == 0:
+                        Kf, Vf = quant.dequant_int8(Kq, Ks), quant.dequant_int8(Vq, Vs)
+                else:
+                    Kq, Ks = quant.quant_int4_per_token(Kx)
+                    Vq, Vs = quant.quant_int4_per_token(Vx)
+                    sets.append((Kq, Vq, Ks, Vs))
+                    if k == 0:
+                        Kf, Vf = quant.dequant_int4(Kq, Ks), quant.dequant_int4(Vq, Vs)
+                del Kx, Vx
+            if fmt == "fp16":
+                fn = lambda i: fq.decode_attn_fp16_mw(q, sets[i][0], sets[i][1], W)
+                nbytes = B * (4 * N * Dm + 4 * Dm)
+            elif fmt == "int8":
+                fn = lambda i: fq.decode_attn_int8_mw(q, sets[i][0], sets[i][1], sets[i][2], sets[i][3], W)
+                nbytes = B * (2 * N * Dm + 4 * N + 4 * Dm)
+            else:
+                fn = lambda i: fq.decode_attn_int4(q, sets[i][0], sets[i][1], sets[i][2], sets[i][3], W)
+                nbytes = B * (N * Dm + 4 * N + 4 * Dm)
+            o = fn(0)
+            ref = _ref_mha(torch, q, Kf, Vf)
+            err = float((o.float() - ref).abs().max())
+            del Kf, Vf, ref
+            ms = _loop_ms(torch, fn, ns, steps, warmup)
+            rows.append(_row("mha_" + fmt, {"B": B, "N": N, "D": Dm, "W": W, "sets": ns}, ms, nbytes, err))
+            log("%-10s B=%-5d N=%d D=%d  %9.2f us  %7.1f GB/s  err %.2e" % (fmt, B, N, Dm, ms * 1e3, nbytes / ms / 1e6, err))
+            del sets
+            torch.cuda.empty_cache()
+
+
+def suite_gqa(torch, fq, steps, warmup, rows):
+    """decode_attn_gqa vs repeat_kv + MHA kernel: Hq=32, Hkv=8, D=64, N=512, B in {1,4,16}."""
+    Hq, Hkv, N, Dg, W = 32, 8, 512, 64, 8
+    G = Hq // Hkv
+    for B in (1, 4, 16):
+        g = torch.Generator(device="cuda").manual_seed(2)
+        per = 2 * B * Hkv * N * Dg * 2
+        ns = _nsets(per)
+        q = torch.randn(B, Hq, Dg, device="cuda", generator=g).half()
+        sets = [(torch.randn(B, Hkv, N, Dg, device="cuda", generator=g).half(),
+                 torch.randn(B, Hkv, N, Dg, device="cuda", generator=g).half()) for _ in range(ns)]
+        K0, V0 = sets[0]
+        Kf = K0.float().repeat_interleave(G, 1).reshape(B * Hq, N, Dg)
+        Vf = V0.float().repeat_interleave(G, 1).reshape(B * Hq, N, Dg)
+        ref = _ref_mha(torch, q.reshape(B * Hq, Dg), Kf, Vf)
+        o = fq.decode_attn_gqa(q, K0, V0, W)
+        err = float((o.reshape(B * Hq, Dg).float() - ref).abs().max())
+        nbytes = B * (4 * Hkv * N * Dg + 4 * Hq * Dg)
+        ms = _loop_ms(torch, lambda i: fq.decode_attn_gqa(q, sets[i][0], sets[i][1], W), ns, steps, warmup)
+        qf = q.reshape(B * Hq, Dg)
+
+        def expand(i):
+            Ke = sets[i][0].repeat_interleave(G, 1).reshape(B * Hq, N, Dg)
+            Ve = sets[i][1].repeat_interleave(G, 1).reshape(B * Hq, N, Dg)
+            return fq.decode_attn_fp16_mw(qf, Ke, Ve, W)
+
+        ms_x = _loop_ms(torch, expand, ns, steps, warmup)
+        rows.append(_row("gqa", {"B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": Dg, "W": W, "sets": ns}, ms, nbytes, err,
+                         expand_mha_us=round(ms_x * 1e3, 3), speedup_vs_expand=round(ms_x / ms, 3)))
+        log("gqa       B=%-3d N=%d D=%d  %8.2f us (repeat_kv + MHA %8.2f us, %.2fx)  err %.2e"
+            % (B, N, Dg, ms * 1e3, ms_x * 1e3, ms_x / ms, err))
+        del sets, Kf, Vf
+
+
+def suite_splitk(torch, fq, steps, warmup, rows):
+    """gqa_sk_fast over N in {512 .. 32K}, D in {64, 128}, best of an S/W sweep; plus B=8, N=32K, D=128."""
+    Hq, Hkv = 32, 8
+    G = Hq // Hkv
+    cases = [(1, N, Dd) for Dd in (64, 128) for N in (512, 1024, 2048, 4096, 8192, 16384, 32768)]
+    cases.append((8, 32768, 128))
+    for B, N, Dd in cases:
+        g = torch.Generator(device="cuda").manual_seed(3)
+        per = 2 * B * Hkv * N * Dd * 2
+        ns = _nsets(per)
+        q = torch.randn(B * Hq, Dd, device="cuda", generator=g).half()
+        sets = [(torch.randn(B * Hkv, N, Dd, device="cuda", generator=g).half(),
+                 torch.randn(B * Hkv, N, Dd, device="cuda", generator=g).half()) for _ in range(ns)]
+        K0, V0 = sets[0]
+        ref = _ref_mha(torch, q, K0.float().repeat_interleave(G, 0), V0.float().repeat_interleave(G, 0))
+        nbytes = B * (4 * Hkv * N * Dd + 4 * Hq * Dd)
+        best = None
+        for S in (8, 16, 32, 64, 128):
+            if S > N // 16:
+                continue
+            for W in (4, 8):
+                mp = torch.empty(B * Hq, S, device="cuda")
+                lp = torch.empty(B * Hq, S, device="cuda")
+                op = torch.empty(B * Hq, S, Dd, device="cuda")
+                o = torch.empty(B * Hq, Dd, device="cuda", dtype=torch.float16)
+                fn = lambda i: fq.gqa_sk_fast(q, sets[i][0], sets[i][1], mp, lp, op, o, S, W, 8)
+                fn(0)
+                err = float((o.float() - ref).abs().max())
+                if err > 2e-3:
+                    log("split-K B=%d N=%d D=%d S%d W%d failed the gate: %.2e" % (B, N, Dd, S, W, err))
+                    continue
+                ms = _loop_ms(torch, fn, ns, max(50, steps // 4), max(10, warmup // 4))
+                if best is None or ms < best[0]:
+                    best = (ms, S, W, err)
+        ms, S, W, err = best
+        # re-time the winner with the full step count
+        mp = torch.empty(B * Hq, S, device="cuda")
+        lp = torch.empty(B * Hq, S, device="cuda")
+        op = torch.empty(B * Hq, S, Dd, device="cuda")
+        o = torch.empty(B * Hq, Dd, device="cuda", dtype=torch.float16)
+        ms = _loop_ms(torch, lambda i: fq.gqa_sk_fast(q, sets[i][0], sets[i][1], mp, lp, op, o, S, W, 8), ns, steps, warmup)
+        rows.append(_row("gqa_sk_fast", {"B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": Dd, "S": S, "W": W, "CW": 8,
+                                         "sets": ns}, ms, nbytes, err))
+        log("split-K   B=%d N=%-6d D=%-3d S%-3d W%d  %8.2f us  %7.1f GB/s  err %.2e" % (B, N, Dd, S, W, ms * 1e3, nbytes / ms / 1e6, err))
+        del sets, ref
+
+
+def suite_mha_small(torch, fq, steps, warmup, rows):
+    """fp16 MHA, 32 heads, N=512, D=128 (the reference's CPU-runnable case)."""
+    B, N, Dm, W = 32, 512, 128, 8
+    g = torch.Generator(device="cuda").manual_seed(4)
+    ns = _nsets(2 * B * N * Dm * 2)
+    q = torch.randn(B, Dm, device="cuda", generator=g).half()
+    sets = [(torch.randn(B, N, Dm, device="cuda", generator=g).half(),
+             torch.randn(B, N, Dm, device="cuda", generator=g).half()) for _ in range(ns)]
+    o = fq.decode_attn_fp16_mw(q, sets[0][0], sets[0][1], W)
+    err = float((o.float() - _ref_mha(torch, q, sets[0][0].float(), sets[0][1].float())).abs().max())
+    nbytes = B * (4 * N * Dm + 4 * Dm)
+    ms = _loop_ms(torch, lambda i: fq.decode_attn_fp16_mw(q, sets[i][0], sets[i][1], W), ns, steps, warmup)
+    rows.append(_row("mha_fp16", {"B": B, "N": N, "D": Dm, "W": W, "sets": ns}, ms, nbytes, err))
+    log("mha_fp16  B=%d N=%d D=%d  %8.2f us  %7.1f GB/s  err %.2e" % (B, N, Dm, ms * 1e3, nbytes / ms / 1e6, err))
+
+
+def run_suite(torch, fq, path, steps=400, warmup=40):
+    rows = []
+    suite_mha_small(torch, fq, steps, warmup, rows)
+    suite_mha_quant(torch, fq, steps, warmup, rows)
+    suite_gqa(torch, fq, steps, warmup, rows)
+    suite_splitk(torch, fq, steps, warmup, rows)
+    with open(path, "w") as f:
+        for r in rows:
+            f.write(json.dumps(r) + "\n")
+    log("suite: %d rows -> %s" % (len(rows), path))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -205,6 +413,8 @@ def main():
     ap.add_argument("--merge", choices=("fused", "two-kernel"), default="fused",
                     help="split merge inside the partial kernel (default) or a separate combine kernel")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--suite", metavar="FILE", default="",
+                    help="also measure the secondary configurations, JSON lines into FILE")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -257,7 +467,12 @@ def main():
     ev = HipEvents()
     p_avg_ms, p_med_ms = time_partial(torch, fq, q, Ks, Vs, S, W, CW, min(args.steps, 1000), ev)
     value = alg_bytes() / ms / 1e6  # GB/s
-    achieved = alg_bytes() / p_avg_ms / 1e6
+    if args.merge == "fused":
+        # one kernel per call: its average duration is the loop time per call
+        k_ms, method = ms, "HIP events around the timed loop of %d calls, one kernel per call" % args.steps
+    else:
+        k_ms, method = p_avg_ms, "HIP events recorded just before and after each partial launch"
+    achieved = alg_bytes() / k_ms / 1e6
     traffic = read_traffic()
     line = {
         "metric": METRIC,
@@ -293,10 +508,17 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
-            "avg_us": round(p_avg_ms * 1e3, 3),
-            "median_us": round(p_med_ms * 1e3, 3),
+            "avg_us": round(k_ms * 1e3, 3),
+            "method": method,
+            "per_launch_event_avg_us": round(p_avg_ms * 1e3, 3),
+            "per_launch_event_median_us": round(p_med_ms * 1e3, 3),
+            "alg_bytes_per_launch": alg_bytes(),
         },
     }
+    if args.suite:
+        del Ks, Vs
+        torch.cuda.empty_cache()
+        run_suite(torch, fq, args.suite)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
