@@ -1,0 +1,153 @@
+"""GPU parity through the C ABI itself (ctypes on libfqkv_decode.so, no PyTorch
+binding in between): every entry point of include/fqkv_decode.h, on device
+buffers from PyTorch, against the float64 oracle at max-abs 2e-3; the
+workspace contract of the single-block calls (enough, too small, none) and
+the dequant helper bit-exact against the oracle's dequantisation."""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import fqkv_decode
+from fqkv_decode import quant
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+I64 = ctypes.c_int64
+VP = ctypes.c_void_p
+SZ = ctypes.c_size_t
+KV_F16, KV_I8, KV_I4 = 0, 1, 2
+
+
+@pytest.fixture(scope="module")
+def lib():
+    L = ctypes.CDLL(fqkv_decode.lib_path())
+    L.fqkv_last_error.restype = ctypes.c_char_p
+    L.fqkv_workspace_bytes.restype = SZ
+    L.fqkv_workspace_bytes.argtypes = [I64, I64, I64, I64, ctypes.c_int, I64]
+    L.fqkv_decode_attn_fp16_mw.argtypes = [VP] * 4 + [I64] * 4 + [VP, SZ, VP]
+    L.fqkv_decode_attn_int8_mw.argtypes = [VP] * 6 + [I64] * 4 + [VP, SZ, VP]
+    L.fqkv_decode_attn_int4.argtypes = [VP] * 6 + [I64] * 4 + [VP, SZ, VP]
+    L.fqkv_decode_attn_gqa.argtypes = [VP] * 4 + [I64] * 6 + [VP, SZ, VP]
+    L.fqkv_gqa_sk_fast.argtypes = [VP] * 7 + [I64] * 7 + [VP]
+    L.fqkv_dequant_kv.argtypes = [VP, VP, VP, I64, I64, ctypes.c_int, ctypes.c_int, VP]
+    return L
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def check(lib, rc):
+    assert rc == 0, lib.fqkv_last_error().decode()
+
+
+def draw(g, *shape):
+    return torch.randn(*shape, generator=g, dtype=torch.float32)
+
+
+def maxerr(out, ref):
+    return float(np.abs(out.float().cpu().numpy().astype(np.float64) - ref).max())
+
+
+def workspace(lib, rows, G, N, D, fmt, W):
+    n = lib.fqkv_workspace_bytes(rows, G, N, D, fmt, W)
+    return torch.empty(max(n, 16), dtype=torch.uint8, device="cuda"), n
+
+
+@pytest.mark.parametrize("B,N,D,W", [(1, 4096, 128, 8), (4, 100, 64, 4), (64, 512, 128, 2)])
+def test_cabi_fp16_mha(lib, B, N, D, W):
+    g = torch.Generator().manual_seed(20)
+    q, K, V = draw(g, B, D).half(), draw(g, B, N, D).half(), draw(g, B, N, D).half()
+    ref = oracle.attention(q.numpy(), K.numpy(), V.numpy())
+    qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
+    ws, n = workspace(lib, B, 1, N, D, KV_F16, W)
+    for wptr, wbytes in ((ws.data_ptr(), n), (ws.data_ptr(), n // 3), (None, 0)):
+        o = torch.empty(B, D, dtype=torch.float16, device="cuda")
+        check(lib, lib.fqkv_decode_attn_fp16_mw(qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), o.data_ptr(),
+                                                B, N, D, W, wptr, wbytes, stream()))
+        torch.cuda.synchronize()
+        assert maxerr(o, ref) <= TOL, (wbytes, maxerr(o, ref))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("B,N,D", [(2, 4096, 128), (16, 300, 64)])
+def test_cabi_quantized_mha(lib, fmt, B, N, D):
+    g = torch.Generator().manual_seed(21)
+    q = draw(g, B, D).half()
+    Kx, Vx = draw(g, B, N, D), draw(g, B, N, D)
+    if fmt == "int8":
+        Kq, Ks = quant.quant_int8_per_token(Kx)
+        Vq, Vs = quant.quant_int8_per_token(Vx)
+        Kf, Vf = quant.dequant_int8(Kq, Ks), quant.dequant_int8(Vq, Vs)
+        f, kind = lib.fqkv_decode_attn_int8_mw, KV_I8
+    else:
+        Kq, Ks = quant.quant_int4_per_token(Kx)
+        Vq, Vs = quant.quant_int4_per_token(Vx)
+        Kf, Vf = quant.dequant_int4(Kq, Ks), quant.dequant_int4(Vq, Vs)
+        f, kind = lib.fqkv_decode_attn_int4, KV_I4
+    ref = oracle.attention(q.numpy(), Kf.numpy(), Vf.numpy())
+    d = [t.cuda() for t in (q, Kq, Vq, Ks, Vs)]
+    ws, n = workspace(lib, B, 1, N, D, kind, 8)
+    o = torch.empty(B, D, dtype=torch.float16, device="cuda")
+    check(lib, f(*[t.data_ptr() for t in d], o.data_ptr(), B, N, D, 8, ws.data_ptr(), n, stream()))
+    torch.cuda.synchronize()
+    assert maxerr(o, ref) <= TOL
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D", [(1, 32, 8, 512, 64), (3, 16, 16, 1000, 128), (2, 24, 2, 77, 128)])
+def test_cabi_gqa(lib, B, Hq, Hkv, N, D):
+    g = torch.Generator().manual_seed(22)
+    q, K, V = draw(g, B, Hq, D).half(), draw(g, B, Hkv, N, D).half(), draw(g, B, Hkv, N, D).half()
+    ref = oracle.gqa_attention(q.numpy(), K.numpy(), V.numpy())
+    qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
+    ws, n = workspace(lib, B * Hkv, Hq // Hkv, N, D, KV_F16, 4)
+    o = torch.empty(B, Hq, D, dtype=torch.float16, device="cuda")
+    check(lib, lib.fqkv_decode_attn_gqa(qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), o.data_ptr(),
+                                        B, Hq, Hkv, N, D, 4, ws.data_ptr(), n, stream()))
+    torch.cuda.synchronize()
+    assert maxerr(o, ref) <= TOL
+
+
+@pytest.mark.parametrize("Hq,Hkv,N,D,S", [(32, 8, 16384, 128, 32), (8, 2, 100, 64, 7), (4, 4, 3, 128, 8)])
+def test_cabi_gqa_sk_fast(lib, Hq, Hkv, N, D, S):
+    g = torch.Generator().manual_seed(23)
+    q, K, V = draw(g, Hq, D).half(), draw(g, Hkv, N, D).half(), draw(g, Hkv, N, D).half()
+    ref = oracle.gqa_attention(q.numpy()[None], K.numpy()[None], V.numpy()[None])[0]
+    m, l, acc = oracle.split_partials(q.numpy(), K.numpy(), V.numpy(), S)
+    qd, Kd, Vd = q.cuda(), K.cuda(), V.cuda()
+    mp = torch.empty(Hq, S, device="cuda")
+    lp = torch.empty(Hq, S, device="cuda")
+    op = torch.empty(Hq, S, D, device="cuda")
+    o = torch.empty(Hq, D, dtype=torch.float16, device="cuda")
+    check(lib, lib.fqkv_gqa_sk_fast(qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), mp.data_ptr(), lp.data_ptr(),
+                                    op.data_ptr(), o.data_ptr(), Hq, Hkv, N, D, S, 8, 8, stream()))
+    torch.cuda.synchronize()
+    assert maxerr(o, ref) <= TOL
+    assert np.array_equal(np.isneginf(mp.cpu().numpy()), np.isneginf(m))
+    np.testing.assert_allclose(lp.cpu().numpy(), l, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(op.cpu().numpy(), acc, rtol=1e-4, atol=2e-4)
+
+
+@pytest.mark.parametrize("fmt", [KV_I8, KV_I4])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("path", [0, 1])
+def test_cabi_dequant_bit_exact(lib, fmt, D, path):
+    g = torch.Generator().manual_seed(24)
+    T = 257
+    X = draw(g, T, D)
+    if fmt == KV_I8:
+        Kq, Ks = quant.quant_int8_per_token(X)
+        ref = oracle.dequant_int8(Kq.numpy(), Ks.numpy())
+    else:
+        Kq, Ks = quant.quant_int4_per_token(X)
+        ref = oracle.dequant_int4(Kq.numpy(), Ks.numpy())
+    out = torch.empty(T, D, device="cuda")
+    Kd, Sd = Kq.cuda(), Ks.cuda()
+    check(lib, lib.fqkv_dequant_kv(Kd.data_ptr(), Sd.data_ptr(), out.data_ptr(), T, D, fmt, path, stream()))
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), ref.astype(np.float32))
