@@ -212,6 +212,67 @@ __device__ void merge_splits(const float* __restrict__ m_part, const float* __re
   }
 }
 
+// Row pitch of the per-wave accumulator rows in LDS: 4 floats of padding
+// spread the wave's float4 writes over more banks.
+template <int D>
+constexpr int opitch() { return D + 4; }
+
+// Merge the NWC waves' (m, l, acc) of a workgroup through LDS and emit the
+// normalised fp16 output (one split) or the split's fp32 partials. Thread
+// (head h, element d) forms the waves' weights e^(m_w - M) itself from the
+// head's LDS row; an empty wave (m = -inf) weighs 0 and an empty split keeps
+// M = -inf with l = acc = 0. All LDS reads are in flight together. A wave
+// covers one head (D threads per head, D >= 64), so the head's global row
+// address is wave-uniform.
+template <int D, int HG, int NWC>
+__device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const float (*s_o)[HG][opitch<D>()],
+                                                 const float (*s_m)[NW_MAX], const float (*s_l)[NW_MAX],
+                                                 size_t qrow0, int hcnt, int s) {
+  for (int idx = threadIdx.x; idx < hcnt * D; idx += blockDim.x) {
+    const int h = __builtin_amdgcn_readfirstlane(idx / D);
+    const int d = idx % D;
+    float mw[NWC], lw[NWC], ow[NWC];
+#pragma unroll
+    for (int ww = 0; ww < NWC; ++ww) {
+      mw[ww] = s_m[h][ww];
+      lw[ww] = s_l[h][ww];
+      ow[ww] = s_o[ww][h][d];
+    }
+    float M = mw[0];
+#pragma unroll
+    for (int ww = 1; ww < NWC; ++ww) M = fmaxf(M, mw[ww]);
+    const float Mu = (M == -INFINITY) ? 0.0f : M;
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int ww = 0; ww < NWC; ++ww) {
+      const float sc = fast_exp2((mw[ww] - Mu) * p.c);
+      L = fmaf(sc, lw[ww], L);
+      O = fmaf(sc, ow[ww], O);
+    }
+    const size_t qh = qrow0 + h;
+    if (p.direct) {
+      p.o[qh * D + d] = (_Float16)(O / L);
+    } else {
+      const size_t b = qh * p.S + s;
+      float* orow = p.o_part + b * D;
+      const float mo = (M == -INFINITY) ? -INFINITY : M * p.scale;
+      if (p.slot >= 0) {  // device-scope stores: read by another workgroup of this launch
+        if (d == 0) {
+          __hip_atomic_store(p.m_part + b, mo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(p.l_part + b, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __hip_atomic_store(orow + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else {
+        if (d == 0) {
+          p.m_part[b] = mo;
+          p.l_part[b] = L;
+        }
+        orow[d] = O;
+      }
+    }
+  }
+}
+
 template <int FMT, int D, int HG>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
@@ -220,7 +281,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   constexpr int U = (FMT == KV_I8 && D == 128) ? 3 : 4;
   constexpr int VE = VG::VE;   // PV steps per tile
   constexpr int VD = VG::VD;   // dwords per V chunk
-  __shared__ float s_o[NW_MAX][HG][D];
+  __shared__ float s_o[NW_MAX][HG][opitch<D>()];
   __shared__ float s_m[HG][NW_MAX];
   __shared__ float s_l[HG][NW_MAX];
   __shared__ fl4_t s_macc[64 * NW_MAX];  // in-kernel split merge
@@ -386,53 +447,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   __syncthreads();
 
   // ---- merge the waves, emit output or split scratch ----
-  // Each (head, d) thread forms the waves' weights e^(m_w - M) itself from
-  // the head's LDS row (an empty wave, m = -inf, weighs 0; an empty split
-  // keeps M = -inf). Unrolled over NW_MAX with selects, so the LDS reads of
-  // all waves are in flight together; slots of absent waves hold stale LDS
-  // and are selected, never multiplied, away.
-  for (int idx = threadIdx.x; idx < hcnt * D; idx += blockDim.x) {
-    const int h = idx / D;
-    const int d = idx - h * D;
-    float mw[NW_MAX], lw[NW_MAX], ow[NW_MAX];
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < NW_MAX; ++ww) {
-      mw[ww] = s_m[h][ww];
-      lw[ww] = s_l[h][ww];
-      ow[ww] = s_o[ww][h][d];
-      if (ww < nw) M = fmaxf(M, mw[ww]);
-    }
-    float L = 0.0f, O = 0.0f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int ww = 0; ww < NW_MAX; ++ww) {
-        const float sc = fast_exp2((mw[ww] - M) * p.c);
-        L += (ww < nw) ? sc * lw[ww] : 0.0f;
-        O += (ww < nw) ? sc * ow[ww] : 0.0f;
-      }
-    }
-    const size_t qh = qrow0 + h;
-    if (p.direct) {
-      p.o[qh * D + d] = (_Float16)(O / L);
-    } else {
-      const size_t b = qh * p.S + s;
-      const float mo = (M == -INFINITY) ? -INFINITY : M * p.scale;
-      if (p.slot >= 0) {  // device-scope stores: read by another workgroup of this launch
-        if (d == 0) {
-          __hip_atomic_store(p.m_part + b, mo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(p.l_part + b, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __hip_atomic_store(p.o_part + b * D + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      } else {
-        if (d == 0) {
-          p.m_part[b] = mo;
-          p.l_part[b] = L;
-        }
-        p.o_part[b * D + d] = O;
-      }
-    }
-  }
+  if (nw == 8)
+    merge_waves_emit<D, HG, 8>(p, s_o, s_m, s_l, qrow0, hcnt, s);
+  else if (nw == 4)
+    merge_waves_emit<D, HG, 4>(p, s_o, s_m, s_l, qrow0, hcnt, s);
+  else
+    merge_waves_emit<D, HG, 2>(p, s_o, s_m, s_l, qrow0, hcnt, s);
 
   // ---- in-kernel split merge: the last of the S workgroups of this
   // (KV row, head group) merges the S partials of its heads. The partials
