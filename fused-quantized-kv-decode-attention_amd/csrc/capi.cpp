@@ -66,12 +66,16 @@ int device_cus(int* out) {
   return FQKV_OK;
 }
 
+// Query heads per workgroup: the transposed-score kernels carry up to 16
+// heads in one matrix-core tile at the same cost, so a group takes all of
+// its KV row's query heads up to 16.
 int choose_hg(int64_t G, int fmt) {
-  if (fmt != KV_F16) return 1;
+  (void)fmt;
   if (G <= 1) return 1;
   if (G == 2) return 2;
   if (G <= 4) return 4;
-  return 8;
+  if (G <= 8) return 8;
+  return 16;
 }
 
 // Splits for the single-block entry points: enough workgroups for about two
@@ -162,6 +166,16 @@ int check_ptrs_kv(const void* q, const void* K, const void* V, const void* o) {
   return FQKV_OK;
 }
 
+int check_ptrs_quant(int fmt, int64_t D, const void* q, const void* K, const void* V, const void* Ks,
+                     const void* Vs, const void* o) {
+  if (!q || !K || !V || !Ks || !Vs || !o) return fail(FQKV_ERR_ARG, "null tensor pointer");
+  const uintptr_t kal = (fmt == KV_I4 && D == 64) ? 8 : 16;
+  if (!aligned(K, kal) || !aligned(V, kal)) return fail(FQKV_ERR_ARG, "K and V must be %d-byte aligned", (int)kal);
+  if (!aligned(q, 16) || !aligned(o, 2) || !aligned(Ks, 2) || !aligned(Vs, 2))
+    return fail(FQKV_ERR_ARG, "q must be 16-byte aligned, o and scales 2-byte aligned");
+  return FQKV_OK;
+}
+
 // The kernels address a KV row block with 32-bit byte offsets.
 int check_span(int64_t N, int64_t D, int fmt) {
   const int64_t row_bytes = fmt == KV_F16 ? 2 * D : (fmt == KV_I8 ? D : D / 2);
@@ -171,22 +185,26 @@ int check_span(int64_t N, int64_t D, int fmt) {
   return FQKV_OK;
 }
 
-int sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l_part,
-            float* o_part, void* o, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int64_t S,
-            int64_t W, int64_t CW, void* stream, void* ev_begin, void* ev_end) {
+int sk_fast(int fmt, const void* q, const void* K, const void* V, const void* Ks, const void* Vs,
+            float* m_part, float* l_part, float* o_part, void* o, int64_t Hq, int64_t Hkv, int64_t N,
+            int64_t D, int64_t S, int64_t W, int64_t CW, void* stream, void* ev_begin, void* ev_end) {
   int rc = check_common(N, D, W);
   if (rc) return rc;
   if (CW != 4 && CW != 8) return fail(FQKV_ERR_ARG, "CW: combine waves must be 4 or 8, got %lld", (long long)CW);
   if (S < 1 || S > (1 << 20)) return fail(FQKV_ERR_ARG, "S: split count must be in [1, 2^20], got %lld", (long long)S);
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
     return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
-  rc = check_ptrs_kv(q, K, V, o);
+  if (fmt == KV_F16) {
+    rc = check_ptrs_kv(q, K, V, o);
+  } else {
+    rc = check_ptrs_quant(fmt, D, q, K, V, Ks, Vs, o);
+  }
   if (rc) return rc;
-  if ((rc = check_span(N, D, KV_F16))) return rc;
+  if ((rc = check_span(N, D, fmt))) return rc;
   if (!m_part || !l_part || !o_part) return fail(FQKV_ERR_ARG, "null scratch pointer");
   if (!aligned(o_part, 16)) return fail(FQKV_ERR_ARG, "o_part must be 16-byte aligned");
   const int64_t G = Hq / Hkv;
-  const int hg = choose_hg(G, KV_F16);
+  const int hg = choose_hg(G, fmt);
   const int64_t ngroups = (G + hg - 1) / hg;
   const int64_t nblocks = Hkv * ngroups * S;
   if (nblocks > INT_MAX || Hq > INT_MAX) return fail(FQKV_ERR_ARG, "problem too large");
@@ -196,6 +214,8 @@ int sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l
   p.q = (const _Float16*)q;
   p.K = (const uint8_t*)K;
   p.V = (const uint8_t*)V;
+  p.Ks = (const _Float16*)Ks;
+  p.Vs = (const _Float16*)Vs;
   p.m_part = m_part;
   p.l_part = l_part;
   p.o_part = o_part;
@@ -213,7 +233,7 @@ int sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l
   p.slot = S > 1 ? merge_slot(Hkv * ngroups) : -1;
   hipError_t e;
   if (ev_begin && (e = hipEventRecord((hipEvent_t)ev_begin, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-  e = launch_partial(KV_F16, (int)D, hg, p, (int)nblocks, (int)W, st);
+  e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)W, st);
   if (e != hipSuccess) return hip_fail(e, "partial");
   if (ev_end && (e = hipEventRecord((hipEvent_t)ev_end, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
   if (p.slot < 0) {
@@ -272,11 +292,7 @@ static int quant_entry(int fmt, const void* q, const void* K, const void* V, con
   int rc = check_common(N, D, W);
   if (rc) return rc;
   if (B < 1) return fail(FQKV_ERR_ARG, "B: batch must be >= 1, got %lld", (long long)B);
-  if (!q || !K || !V || !Ks || !Vs || !o) return fail(FQKV_ERR_ARG, "null tensor pointer");
-  const uintptr_t kal = (fmt == KV_I4 && D == 64) ? 8 : 16;
-  if (!aligned(K, kal) || !aligned(V, kal)) return fail(FQKV_ERR_ARG, "K and V must be %d-byte aligned", (int)kal);
-  if (!aligned(q, 16) || !aligned(o, 2) || !aligned(Ks, 2) || !aligned(Vs, 2))
-    return fail(FQKV_ERR_ARG, "q must be 16-byte aligned, o and scales 2-byte aligned");
+  if ((rc = check_ptrs_quant(fmt, D, q, K, V, Ks, Vs, o))) return rc;
   if ((rc = check_span(N, D, fmt))) return rc;
   return run_decode(fmt, q, K, V, Ks, Vs, o, B, 1, N, D, W, workspace, workspace_bytes,
                     (hipStream_t)stream);
@@ -311,14 +327,43 @@ int fqkv_decode_attn_gqa(const void* q, const void* K, const void* V, void* o, i
 int fqkv_gqa_sk_fast(const void* q, const void* K, const void* V, float* m_part, float* l_part,
                      float* o_part, void* o, int64_t Hq, int64_t Hkv, int64_t N, int64_t D,
                      int64_t S, int64_t W, int64_t CW, void* stream) {
-  return sk_fast(q, K, V, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW, stream, nullptr, nullptr);
+  return sk_fast(KV_F16, q, K, V, nullptr, nullptr, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW,
+                 stream, nullptr, nullptr);
 }
 
 int fqkv_gqa_sk_fast_timed(const void* q, const void* K, const void* V, float* m_part,
                            float* l_part, float* o_part, void* o, int64_t Hq, int64_t Hkv,
                            int64_t N, int64_t D, int64_t S, int64_t W, int64_t CW, void* stream,
                            void* ev_begin, void* ev_end) {
-  return sk_fast(q, K, V, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW, stream, ev_begin, ev_end);
+  return sk_fast(KV_F16, q, K, V, nullptr, nullptr, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW,
+                 stream, ev_begin, ev_end);
+}
+
+int fqkv_decode_attn_gqa_quant(const void* q, const void* K, const void* V, const void* Ks,
+                               const void* Vs, void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
+                               int64_t D, int kv_format, int64_t W, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  int rc = check_common(N, D, W);
+  if (rc) return rc;
+  if (B < 1) return fail(FQKV_ERR_ARG, "B: batch must be >= 1, got %lld", (long long)B);
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
+    return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
+  if ((rc = check_ptrs_quant(kv_format, D, q, K, V, Ks, Vs, o))) return rc;
+  if ((rc = check_span(N, D, kv_format))) return rc;
+  return run_decode(kv_format, q, K, V, Ks, Vs, o, B * Hkv, Hq / Hkv, N, D, W, workspace,
+                    workspace_bytes, (hipStream_t)stream);
+}
+
+int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const void* Ks, const void* Vs,
+                           float* m_part, float* l_part, float* o_part, void* o, int64_t Hq,
+                           int64_t Hkv, int64_t N, int64_t D, int kv_format, int64_t S, int64_t W,
+                           int64_t CW, void* stream) {
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  return sk_fast(kv_format, q, K, V, Ks, Vs, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW, stream,
+                 nullptr, nullptr);
 }
 
 int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, int64_t D,
@@ -334,6 +379,26 @@ int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, 
   if (!aligned(Ks, 2) || !aligned(out, 4)) return fail(FQKV_ERR_ARG, "misaligned scale or output pointer");
   hipError_t e = launch_dequant(kv_format, (int)D, path, Kq, Ks, out, tokens, (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "launch: dequant kernel");
+  return FQKV_OK;
+}
+
+int fqkv_quantize_kv(const void* X, int x_dtype, void* Q, void* scales, int64_t tokens, int64_t D,
+                     int kv_format, void* stream) {
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32)
+    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16 or FQKV_SRC_F32");
+  if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
+  if (tokens < 1) return fail(FQKV_ERR_ARG, "tokens must be >= 1, got %lld", (long long)tokens);
+  if (!X || !Q || !scales) return fail(FQKV_ERR_ARG, "null tensor pointer");
+  const uintptr_t xal = (x_dtype == FQKV_SRC_F16 && D == 64) ? 8 : 16;
+  const uintptr_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
+  if (!aligned(X, xal)) return fail(FQKV_ERR_ARG, "X must be %d-byte aligned", (int)xal);
+  if (!aligned(Q, qal)) return fail(FQKV_ERR_ARG, "Q must be %d-byte aligned", (int)qal);
+  if (!aligned(scales, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
+  hipError_t e = launch_quantize(x_dtype == FQKV_SRC_F16, kv_format, (int)D, X, Q, scales, tokens,
+                                 (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "launch: quantize kernel");
   return FQKV_OK;
 }
 

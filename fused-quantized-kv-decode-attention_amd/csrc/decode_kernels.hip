@@ -321,6 +321,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   }
 
   float m_run = -INFINITY, l_run = 0.0f;  // of head n, over the tokens this lane scored
+  int acc_shift = 0;                      // acc holds the true accumulators times 2^acc_shift
   f4_t acc[VE];                           // O^T: step c, reg k = head-dim VE (4R + k) + c of head n
 #pragma unroll
   for (int c = 0; c < VE; ++c) acc[c] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
@@ -394,9 +395,25 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     const float mn = fmaxf(m_run, rows4_max(mx));
     const float mu = (mn == -INFINITY) ? 0.0f : mn;
     const float alpha = fast_exp2((m_run - mu) * p.c);
-    // The PV operand carries each fp32 weight as an fp16 pair hi + lo
-    // (hi = fp16(w), lo = fp16(w - hi)): two matrix-core steps reproduce the
-    // fp32 weight to ~2^-22 relative, V being exact in fp16.
+    // The PV operand carries each fp32 weight w = p * (V scale) as an fp16
+    // pair hi + lo (hi = fp16(w'), lo = fp16(w' - hi)) of w' = w * 2^shift:
+    // two matrix-core steps reproduce the weight to ~2^-22 relative, V being
+    // exact in fp16. The power-of-two shift puts the pass's largest possible
+    // weight just under 2^14, so lo stays clear of the fp16 subnormals (small
+    // per-token scales would otherwise push it there); acc is kept in units
+    // of 2^shift and rescaled exactly when the shift changes.
+    int shift = 13;  // fp16 KV: w = p <= 1
+    if constexpr (F::QUANT) {
+      float vmax = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) vmax = fmaxf(vmax, (float)vs[u][k]);
+      vmax = rows4_max(vmax);
+      // vmax < 2^e with e from the exponent field (vmax is a normal fp32)
+      const int e = vmax > 0.0f ? (int)((__builtin_bit_cast(uint32_t, vmax) >> 23) & 0xFFu) - 126 : 0;
+      shift = 14 - e;
+    }
     h4_t phi[U], plo[U];
     float psum = 0.0f;
 #pragma unroll
@@ -405,15 +422,17 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       for (int k = 0; k < 4; ++k) {
         const float pw = fast_exp2((x[u][k] - mu) * p.c);
         psum += pw;
-        const float wv = pw * (float)vs[u][k];
+        const float wv = __builtin_amdgcn_ldexpf(pw * (float)vs[u][k], shift);
         const _Float16 h = (_Float16)wv;
         phi[u][k] = h;
         plo[u][k] = (_Float16)(wv - (float)h);
       }
     l_run = l_run * alpha + psum;
     m_run = mn;
+    const float acc_alpha = __builtin_amdgcn_ldexpf(alpha, shift - acc_shift);
+    acc_shift = shift;
 #pragma unroll
-    for (int c = 0; c < VE; ++c) acc[c] *= alpha;
+    for (int c = 0; c < VE; ++c) acc[c] *= acc_alpha;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
@@ -431,6 +450,10 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 
   // ---- wave totals: l over the four lane rows; O^T rows are disjoint ----
   l_run = rows4_sum(l_run);
+#pragma unroll
+  for (int c = 0; c < VE; ++c)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) acc[c][k] = __builtin_amdgcn_ldexpf(acc[c][k], -acc_shift);
   if (n < HG && n < hcnt) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -534,16 +557,12 @@ static hipError_t launch_partial_t(const PartialParams& p, int nblocks, int nw, 
 
 template <int FMT, int D>
 static hipError_t launch_partial_d(int hg, const PartialParams& p, int nblocks, int nw, hipStream_t st) {
-  if constexpr (FMT == KV_F16) {
-    switch (hg) {
-      case 1: return launch_partial_t<FMT, D, 1>(p, nblocks, nw, st);
-      case 2: return launch_partial_t<FMT, D, 2>(p, nblocks, nw, st);
-      case 4: return launch_partial_t<FMT, D, 4>(p, nblocks, nw, st);
-      case 8: return launch_partial_t<FMT, D, 8>(p, nblocks, nw, st);
-      case 16: return launch_partial_t<FMT, D, 16>(p, nblocks, nw, st);
-    }
-  } else {
-    if (hg == 1) return launch_partial_t<FMT, D, 1>(p, nblocks, nw, st);
+  switch (hg) {
+    case 1: return launch_partial_t<FMT, D, 1>(p, nblocks, nw, st);
+    case 2: return launch_partial_t<FMT, D, 2>(p, nblocks, nw, st);
+    case 4: return launch_partial_t<FMT, D, 4>(p, nblocks, nw, st);
+    case 8: return launch_partial_t<FMT, D, 8>(p, nblocks, nw, st);
+    case 16: return launch_partial_t<FMT, D, 16>(p, nblocks, nw, st);
   }
   return hipErrorInvalidValue;
 }

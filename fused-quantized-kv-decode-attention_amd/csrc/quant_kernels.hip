@@ -1,0 +1,184 @@
+// gfx950 per-token KV quantizers: the on-GPU producers of the int8 / int4 KV
+// formats the decode kernels read.
+//
+// Reference expressions (PyTorch, evaluated in the input's dtype):
+//   int8: tests/test_kernels.py:32-34 -- s = max|x| / 127 clamped to >= 1e-8,
+//         q = clamp(round(x / s), -127, 127), scales stored as fp16;
+//   int4: nb:292-299 -- the same with 7, values packed two per byte, low
+//         nibble = even element.
+// The kernels reproduce those bytes exactly:
+//   * the reference runs them on CUDA tensors, where PyTorch evaluates
+//     a / qmax (tensor by Python scalar) as a * fp32(1/qmax), and x / s (tensor
+//     by tensor) as a true division;
+//   * fp32 input: s = max(a * fp32(1/qmax), 1e-8) and x / s in IEEE fp32
+//     (correctly rounded division), round-half-even (v_rndne_f32), clamp,
+//     scale = fp16(s);
+//   * fp16 input: PyTorch evaluates each fp16 op in fp32 and rounds the result
+//     to fp16, so s = fp16(a * fp32(1/qmax)) and every quotient is rounded to
+//     fp16 before the round-half-even. A row whose fp16 scale underflows to 0 (max|x|
+//     below ~4e-6) would divide by zero in the reference; here x = 0 maps to 0
+//     and other x to +-qmax, the reference's clamp of +-inf.
+//
+// Layout: 16 lanes own one token row (D/16 consecutive elements each); a wave
+// covers 4 rows per step, a 256-thread workgroup 16, grid-striding over rows.
+// The row maximum is a DPP all-reduce within the 16-lane row. HBM-bound:
+// reads 2 or 4 B per element, writes 1 or 0.5 B per element + 2 B per row.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "kv_formats.h"
+#include "launch.h"
+
+namespace fqkv {
+
+namespace {
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+// Max over each 16-lane row: quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror.
+__device__ __forceinline__ float row16_max(float x) {
+  x = fmaxf(x, dpp_f<0xB1>(x));
+  x = fmaxf(x, dpp_f<0x4E>(x));
+  x = fmaxf(x, dpp_f<0x141>(x));
+  return fmaxf(x, dpp_f<0x140>(x));
+}
+
+template <bool F16, int EPL>
+__device__ __forceinline__ void load_row_slice(const void* X, int64_t row, int i, int D, float (&x)[EPL]) {
+  if constexpr (F16) {
+    const _Float16* p = (const _Float16*)X + row * D + EPL * i;
+    if constexpr (EPL == 8) {
+      const h8_t v = *(const h8_t*)p;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const _Float16 h = v[e];
+        x[e] = (float)h;
+      }
+    } else {
+      typedef _Float16 h4v_t __attribute__((ext_vector_type(4)));
+      const h4v_t v = *(const h4v_t*)p;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const _Float16 h = v[e];
+        x[e] = (float)h;
+      }
+    }
+  } else {
+    const float* p = (const float*)X + row * D + EPL * i;
+#pragma unroll
+    for (int k = 0; k < EPL / 4; ++k) {
+      const f4_t v = *(const f4_t*)(p + 4 * k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float f = v[e];
+        x[4 * k + e] = f;
+      }
+    }
+  }
+}
+
+template <bool F16, int QMAX, int D>
+__global__ void __launch_bounds__(256) quantize_kernel(const void* __restrict__ X, uint8_t* __restrict__ Q,
+                                                       _Float16* __restrict__ scales, int64_t tokens) {
+  constexpr int EPL = D / 16;  // elements per lane
+  const int i = threadIdx.x & 15;
+  const int64_t rows_per_step = (int64_t)gridDim.x * (blockDim.x >> 4);
+  for (int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
+       row - (threadIdx.x >> 4) < tokens; row += rows_per_step) {
+    // whole 16-lane rows stay active through the DPP reduction; a row past
+    // the end reads nothing and stores nothing
+    const bool live = row < tokens;
+    float x[EPL];
+    if (live) {
+      load_row_slice<F16, EPL>(X, row, i, D, x);
+    } else {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) x[e] = 0.0f;
+    }
+    float a = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) a = fmaxf(a, fabsf(x[e]));
+    a = row16_max(a);
+
+    float s;          // the divisor, as the reference holds it
+    _Float16 s_out;   // the stored scale
+    if constexpr (F16) {
+      s_out = (_Float16)(a * (1.0f / (float)QMAX));  // fp16 op: fp32 result rounded to fp16
+      s = (float)s_out;                      // clamp(min=1e-8) cannot lift an fp16 value
+    } else {
+      s = fmaxf(a * (1.0f / (float)QMAX), 1e-8f);
+      s_out = (_Float16)s;
+    }
+    int q[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      float quot;
+      if constexpr (F16) {
+        if (s == 0.0f) {
+          quot = x[e] == 0.0f ? 0.0f : copysignf((float)QMAX, x[e]);
+        } else {
+          quot = (float)(_Float16)(x[e] / s);
+        }
+      } else {
+        quot = x[e] / s;
+      }
+      const float r = fminf(fmaxf(__builtin_rintf(quot), -(float)QMAX), (float)QMAX);
+      q[e] = (int)r;
+    }
+    if (!live) continue;
+    if constexpr (QMAX == 127) {
+      uint32_t w[EPL / 4];
+#pragma unroll
+      for (int k = 0; k < EPL / 4; ++k)
+        w[k] = (uint32_t)(q[4 * k] & 0xFF) | ((uint32_t)(q[4 * k + 1] & 0xFF) << 8) |
+               ((uint32_t)(q[4 * k + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * k + 3] & 0xFF) << 24);
+      uint8_t* dst = Q + row * D + EPL * i;
+      if constexpr (EPL == 8) {
+        *(u2_t*)dst = u2_t{w[0], w[1]};
+      } else {
+        *(uint32_t*)dst = w[0];
+      }
+    } else {
+      uint32_t w = 0;
+#pragma unroll
+      for (int t = 0; t < EPL / 2; ++t)
+        w |= ((uint32_t)(q[2 * t] & 0xF) | ((uint32_t)(q[2 * t + 1] & 0xF) << 4)) << (8 * t);
+      uint8_t* dst = Q + row * (D / 2) + (EPL / 2) * i;
+      if constexpr (EPL == 8) {
+        *(uint32_t*)dst = w;
+      } else {
+        *(uint16_t*)dst = (uint16_t)w;
+      }
+    }
+    if (i == 0) scales[row] = s_out;
+  }
+}
+
+template <bool F16, int QMAX>
+hipError_t launch_q(int D, const void* X, void* Q, void* S, int64_t tokens, hipStream_t st) {
+  const int64_t want = (tokens + 15) / 16;
+  const unsigned grid = (unsigned)(want < (1 << 16) ? want : (1 << 16));
+  if (D == 128)
+    hipLaunchKernelGGL((quantize_kernel<F16, QMAX, 128>), dim3(grid), dim3(256), 0, st, X, (uint8_t*)Q,
+                       (_Float16*)S, tokens);
+  else
+    hipLaunchKernelGGL((quantize_kernel<F16, QMAX, 64>), dim3(grid), dim3(256), 0, st, X, (uint8_t*)Q,
+                       (_Float16*)S, tokens);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_quantize(int src_f16, int fmt, int D, const void* X, void* Q, void* S, int64_t tokens,
+                           hipStream_t st) {
+  if (tokens < 1 || (D != 64 && D != 128)) return hipErrorInvalidValue;
+  if (fmt == KV_I8) return src_f16 ? launch_q<true, 127>(D, X, Q, S, tokens, st) : launch_q<false, 127>(D, X, Q, S, tokens, st);
+  if (fmt == KV_I4) return src_f16 ? launch_q<true, 7>(D, X, Q, S, tokens, st) : launch_q<false, 7>(D, X, Q, S, tokens, st);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace fqkv

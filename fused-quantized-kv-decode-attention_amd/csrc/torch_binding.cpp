@@ -202,6 +202,107 @@ void gqa_sk_fast_timed(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch:
            "launch");
 }
 
+// ---- quantized GQA and split-K (no counterpart in the reference) ----
+
+// dtype of an int8 / packed-int4 K, V pair; returns the unpacked head_dim.
+int64_t quant_kv_dims(int fmt, const torch::Tensor& K, const torch::Tensor& V) {
+  if (fmt == FQKV_KV_I8) {
+    TORCH_CHECK(K.scalar_type() == torch::kChar && V.scalar_type() == torch::kChar, "int8: K and V must be int8");
+  } else {
+    TORCH_CHECK(K.scalar_type() == torch::kByte && V.scalar_type() == torch::kByte,
+                "packed uint8: K and V must be uint8 holding two int4 values per byte");
+  }
+  TORCH_CHECK(V.sizes() == K.sizes(), "shape: K and V must have the same shape; got ", K.sizes(), " and ",
+              V.sizes());
+  const int64_t D = fmt == FQKV_KV_I8 ? K.size(-1) : 2 * K.size(-1);
+  check_D(D);
+  return D;
+}
+
+// decode_attn_gqa_int8 / _int4 (q[B,Hq,D], K[B,Hkv,N,D or D/2], V, Ks[B,Hkv,N] fp16, Vs, W) -> o[B,Hq,D]
+torch::Tensor decode_attn_gqa_quant(int fmt, torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks,
+                                    torch::Tensor Vs, int64_t W) {
+  check_gpu({&q, &K, &V, &Ks, &Vs});
+  check_half(q, "q");
+  check_half(Ks, "Ks");
+  check_half(Vs, "Vs");
+  TORCH_CHECK(q.dim() == 3 && K.dim() == 4 && q.size(0) == K.size(0),
+              "shape: expected q [B,Hq,D], K and V [B,Hkv,N,", fmt == FQKV_KV_I8 ? "D" : "D/2", "]; got q ",
+              q.sizes(), ", K ", K.sizes());
+  const int64_t D = quant_kv_dims(fmt, K, V);
+  const int64_t B = q.size(0), Hq = q.size(1), Hkv = K.size(1), N = K.size(2);
+  TORCH_CHECK(q.size(2) == D, "shape: q head_dim ", q.size(2), " does not match KV head_dim ", D);
+  TORCH_CHECK(Ks.dim() == 3 && Ks.size(0) == B && Ks.size(1) == Hkv && Ks.size(2) == N && Vs.sizes() == Ks.sizes(),
+              "shape: expected per-token scales Ks and Vs [B,Hkv,N]; got ", Ks.sizes(), " and ", Vs.sizes());
+  check_W(W);
+  TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
+  TORCH_CHECK(N >= 1, "N: need at least one cached token");
+  const c10::DeviceGuard guard(q.device());
+  auto o = torch::empty({B, Hq, D}, q.options());
+  auto ws = workspace_for(q, B * Hkv, Hq / Hkv, N, D, fmt, W);
+  check_rc(fqkv_decode_attn_gqa_quant(q.data_ptr(), K.data_ptr(), V.data_ptr(), Ks.data_ptr(), Vs.data_ptr(),
+                                      o.data_ptr(), B, Hq, Hkv, N, D, fmt, W,
+                                      ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0,
+                                      cur_stream(q)),
+           "launch");
+  return o;
+}
+
+torch::Tensor decode_attn_gqa_int8(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks,
+                                   torch::Tensor Vs, int64_t W) {
+  return decode_attn_gqa_quant(FQKV_KV_I8, q, K, V, Ks, Vs, W);
+}
+torch::Tensor decode_attn_gqa_int4(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks,
+                                   torch::Tensor Vs, int64_t W) {
+  return decode_attn_gqa_quant(FQKV_KV_I4, q, K, V, Ks, Vs, W);
+}
+
+// gqa_sk_fast_int8 / _int4 (q[Hq,D], K[Hkv,N,D or D/2], V, Ks[Hkv,N], Vs, m_part, l_part, o_part, o, S, W, CW)
+void gqa_sk_fast_quant(int fmt, torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks,
+                       torch::Tensor Vs, torch::Tensor m_part, torch::Tensor l_part, torch::Tensor o_part,
+                       torch::Tensor o, int64_t S, int64_t W, int64_t CW) {
+  check_gpu({&q, &K, &V, &Ks, &Vs, &m_part, &l_part, &o_part, &o});
+  check_half(q, "q");
+  check_half(o, "o");
+  check_half(Ks, "Ks");
+  check_half(Vs, "Vs");
+  TORCH_CHECK(m_part.scalar_type() == torch::kFloat && l_part.scalar_type() == torch::kFloat &&
+                  o_part.scalar_type() == torch::kFloat,
+              "partial: m_part, l_part and o_part must be float32");
+  TORCH_CHECK(q.dim() == 2 && K.dim() == 3, "shape: expected q [Hq,D], K and V [Hkv,N,",
+              fmt == FQKV_KV_I8 ? "D" : "D/2", "]; got q ", q.sizes(), ", K ", K.sizes());
+  const int64_t D = quant_kv_dims(fmt, K, V);
+  const int64_t Hq = q.size(0), Hkv = K.size(0), N = K.size(1);
+  TORCH_CHECK(q.size(1) == D, "shape: q head_dim ", q.size(1), " does not match KV head_dim ", D);
+  TORCH_CHECK(Ks.dim() == 2 && Ks.size(0) == Hkv && Ks.size(1) == N && Vs.sizes() == Ks.sizes(),
+              "shape: expected per-token scales Ks and Vs [Hkv,N]; got ", Ks.sizes(), " and ", Vs.sizes());
+  check_W(W);
+  TORCH_CHECK(CW == 4 || CW == 8, "CW: must be 4 or 8, got ", CW);
+  TORCH_CHECK(S >= 1, "S: split count must be >= 1, got ", S);
+  TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
+  TORCH_CHECK(N >= 1, "N: need at least one cached token");
+  TORCH_CHECK(m_part.numel() == Hq * S && l_part.numel() == Hq * S,
+              "partial: m_part and l_part must hold Hq*S = ", Hq * S, " floats");
+  TORCH_CHECK(o_part.numel() == Hq * S * D, "partial: o_part must hold Hq*S*D = ", Hq * S * D, " floats");
+  TORCH_CHECK(o.numel() == Hq * D, "combine: o must hold Hq*D = ", Hq * D, " halves");
+  const c10::DeviceGuard guard(q.device());
+  check_rc(fqkv_gqa_sk_fast_quant(q.data_ptr(), K.data_ptr(), V.data_ptr(), Ks.data_ptr(), Vs.data_ptr(),
+                                  m_part.data_ptr<float>(), l_part.data_ptr<float>(), o_part.data_ptr<float>(),
+                                  o.data_ptr(), Hq, Hkv, N, D, fmt, S, W, CW, cur_stream(q)),
+           "launch");
+}
+
+void gqa_sk_fast_int8(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks, torch::Tensor Vs,
+                      torch::Tensor m_part, torch::Tensor l_part, torch::Tensor o_part, torch::Tensor o, int64_t S,
+                      int64_t W, int64_t CW) {
+  gqa_sk_fast_quant(FQKV_KV_I8, q, K, V, Ks, Vs, m_part, l_part, o_part, o, S, W, CW);
+}
+void gqa_sk_fast_int4(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks, torch::Tensor Vs,
+                      torch::Tensor m_part, torch::Tensor l_part, torch::Tensor o_part, torch::Tensor o, int64_t S,
+                      int64_t W, int64_t CW) {
+  gqa_sk_fast_quant(FQKV_KV_I4, q, K, V, Ks, Vs, m_part, l_part, o_part, o, S, W, CW);
+}
+
 // Dequantise int8 [T,D] / int4 [T,D/2] KV through the kernels' conversions.
 torch::Tensor dequant_kv(torch::Tensor Kq, torch::Tensor Ks, int64_t path) {
   check_gpu({&Kq, &Ks});
@@ -235,6 +336,39 @@ int64_t cu_count() {
 
 }  // namespace
 
+// Per-token KV quantizers on the GPU (fqkv_quantize_kv): the kernel-backed
+// producers of the int8 / int4 formats, bit-identical to the reference's
+// PyTorch expressions (tests/test_kernels.py:32-34, nb:292-299).
+static std::vector<torch::Tensor> quantize_per_token(torch::Tensor X, int fmt) {
+  check_gpu({&X});
+  TORCH_CHECK(X.scalar_type() == torch::kHalf || X.scalar_type() == torch::kFloat,
+              "fp16: X must be float16 or float32");
+  TORCH_CHECK(X.is_contiguous(), "contig: X must be contiguous");
+  TORCH_CHECK(X.dim() >= 1, "shape: X must be [..., D]");
+  const int64_t D = X.size(-1);
+  check_D(D);
+  const int64_t tokens = X.numel() / D;
+  TORCH_CHECK(tokens >= 1, "shape: X must hold at least one token row");
+  const c10::DeviceGuard guard(X.device());
+  auto qsizes = X.sizes().vec();
+  if (fmt == FQKV_KV_I4) qsizes.back() = D / 2;
+  auto Q = torch::empty(qsizes, X.options().dtype(fmt == FQKV_KV_I8 ? torch::kChar : torch::kByte));
+  auto ssizes = X.sizes().vec();
+  ssizes.pop_back();
+  auto S = torch::empty(ssizes, X.options().dtype(torch::kHalf));
+  check_rc(fqkv_quantize_kv(X.data_ptr(), X.scalar_type() == torch::kHalf ? FQKV_SRC_F16 : FQKV_SRC_F32,
+                            Q.data_ptr(), S.data_ptr(), tokens, D, fmt, cur_stream(X)),
+           "launch");
+  return {Q, S};
+}
+
+static std::vector<torch::Tensor> quantize_int8_per_token(torch::Tensor X) {
+  return quantize_per_token(X, FQKV_KV_I8);
+}
+static std::vector<torch::Tensor> quantize_int4_per_token(torch::Tensor X) {
+  return quantize_per_token(X, FQKV_KV_I4);
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "MI355X fused single-query decode attention (fp16 / int8-KV / int4-KV / GQA / GQA split-K)";
   m.def("decode_attn_fp16_mw", &decode_attn_fp16_mw, "fp16 fused decode", py::arg("q"), py::arg("K"), py::arg("V"),
@@ -250,6 +384,20 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("W"), py::arg("CW"));
   m.def("_gqa_sk_fast_timed", &gqa_sk_fast_timed, "gqa_sk_fast with events around the partial kernel");
   m.def("_dequant_kv", &dequant_kv, "dequantise int8/int4 KV through the kernels' conversions");
+  m.def("decode_attn_gqa_int8", &decode_attn_gqa_int8, "GQA-aware int8-KV decode", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("W"));
+  m.def("decode_attn_gqa_int4", &decode_attn_gqa_int4, "GQA-aware int4-KV decode", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("W"));
+  m.def("gqa_sk_fast_int8", &gqa_sk_fast_int8, "GQA split-K int8-KV decode", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("m_part"), py::arg("l_part"), py::arg("o_part"),
+        py::arg("o"), py::arg("S"), py::arg("W"), py::arg("CW"));
+  m.def("gqa_sk_fast_int4", &gqa_sk_fast_int4, "GQA split-K int4-KV decode", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("m_part"), py::arg("l_part"), py::arg("o_part"),
+        py::arg("o"), py::arg("S"), py::arg("W"), py::arg("CW"));
+  m.def("quantize_int8_per_token", &quantize_int8_per_token,
+        "per-token int8 KV quantizer on the GPU -> (int8 [..., D], fp16 scales [...])", py::arg("X"));
+  m.def("quantize_int4_per_token", &quantize_int4_per_token,
+        "per-token int4 KV quantizer on the GPU -> (packed uint8 [..., D/2], fp16 scales [...])", py::arg("X"));
   m.def("_choose_splits", &choose_splits, "split count the single-block entry points use");
   m.def("_cu_count", &cu_count, "compute units of the current device");
   m.def("_version", []() { return std::string(fqkv_version()); });

@@ -10,6 +10,15 @@ Drop-in for the reference's five PyTorch-extension entry points
     gqa_sk_fast(q[Hq,D], K[Hkv,N,D], V, m_part, l_part, o_part, o, S, W, CW) -> None
                                                                       (decode_attn_gqa_sk_fast.cu:95)
 
+Beyond the reference (same conventions, no counterpart there):
+
+    decode_attn_gqa_int8 / decode_attn_gqa_int4(q[B,Hq,D], K[B,Hkv,N,D or D/2], V,
+        Ks[B,Hkv,N], Vs, W) -> o[B,Hq,D]           GQA head mapping over an int8 / int4 cache
+    gqa_sk_fast_int8 / gqa_sk_fast_int4(q[Hq,D], K[Hkv,N,D or D/2], V, Ks[Hkv,N], Vs,
+        m_part, l_part, o_part, o, S, W, CW)        split-K over an int8 / int4 cache
+    quantize_int8_per_token / quantize_int4_per_token(X[..., D]) -> (bytes, fp16 scales)
+                                                    the KV quantizers as GPU kernels
+
 Callers of the reference build each kernel with
 ``torch.utils.cpp_extension.load(name=..., sources=["kernels/<file>.cu"], ...)``
 and call ``m.<function>(...)``; :func:`load` returns the module that serves
@@ -33,13 +42,20 @@ __all__ = [
     "decode_attn_int4",
     "decode_attn_gqa",
     "gqa_sk_fast",
+    "decode_attn_gqa_int8",
+    "decode_attn_gqa_int4",
+    "gqa_sk_fast_int8",
+    "gqa_sk_fast_int4",
+    "quantize_int8_per_token",
+    "quantize_int4_per_token",
     "load",
     "lib_path",
     "ext_path",
 ]
 
 _ENTRY_POINTS = ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa",
-                 "gqa_sk_fast")
+                 "gqa_sk_fast", "decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8",
+                 "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token")
 _EXT = None
 
 

@@ -4,8 +4,9 @@ PyTorch tensor code, as in the reference, so the bytes match the reference's
 on any device for fp16 and fp32 inputs alike:
 
 * int8: tests/test_kernels.py:32-34 (nb:236-238) -- scale = max|x|/127
-  clamped to >= 1e-8, values round(x/scale) clamped to [-127, 127], scales
-  stored as fp16 [.., N].
+  (evaluated, as PyTorch does on the reference's CUDA tensors, as
+  max|x| * fp32(1/127)) clamped to >= 1e-8, values round(x/scale) clamped to
+  [-127, 127], scales stored as fp16 [.., N].
 * int4: nb:292-299 -- scale = max|x|/7, values clamped to [-7, 7], packed two
   per byte with the low nibble holding the even element.
 * dequantisation: nb:301-307 and decode_attn_int8_mw.cu:24,31 --
@@ -16,8 +17,11 @@ import torch
 
 
 def _scales(X, qmax):
+    # The reference writes a / qmax on CUDA tensors, which PyTorch evaluates
+    # as a * fp32(1/qmax); writing the multiplication makes CPU tensors round
+    # the same way, so the bytes do not depend on the device.
     a = X.abs().amax(-1, keepdim=True)
-    s = (a / float(qmax)).clamp(min=1e-8)
+    s = (a * (1.0 / float(qmax))).clamp(min=1e-8)
     return s
 
 

@@ -46,6 +46,8 @@ enum {
 
 enum { FQKV_KV_F16 = 0, FQKV_KV_I8 = 1, FQKV_KV_I4 = 2 };
 
+enum { FQKV_SRC_F16 = 0, FQKV_SRC_F32 = 1 }; /* element type of a quantizer input */
+
 /* Message for the last failing call on this thread ("" if none). */
 const char* fqkv_last_error(void);
 
@@ -118,6 +120,33 @@ int fqkv_gqa_sk_fast(const void* q, const void* K, const void* V, float* m_part,
                      int64_t S, int64_t W, int64_t CW, void* stream);
 
 /*
+ * GQA-aware decode over an int8 or int4 KV cache (kv_format FQKV_KV_I8 /
+ * FQKV_KV_I4) with per-token fp16 scales: the GQA head mapping of
+ * fqkv_decode_attn_gqa with the KV format of fqkv_decode_attn_int8_mw /
+ * fqkv_decode_attn_int4. q: [B, Hq, D] fp16; K, V: [B, Hkv, N, D] int8 or
+ * [B, Hkv, N, D/2] uint8; Ks, Vs: [B, Hkv, N] fp16; o: [B, Hq, D] fp16.
+ * No counterpart in the reference, whose int8/int4 kernels are MHA only
+ * (decode_attn_int8_mw.cu:52-64, decode_attn_int4.cu:47-57) and whose GQA
+ * kernel is fp16 only (decode_attn_gqa.cu:56-68).
+ */
+int fqkv_decode_attn_gqa_quant(const void* q, const void* K, const void* V, const void* Ks,
+                               const void* Vs, void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
+                               int64_t D, int kv_format, int64_t W, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/*
+ * GQA split-K decode over an int8 or int4 KV cache: fqkv_gqa_sk_fast with K,
+ * V in the quantized layout above and per-token scales Ks, Vs [Hkv, N] fp16
+ * (batch folded into the head axis as for fqkv_gqa_sk_fast). Same scratch
+ * layout and semantics. No counterpart in the reference (its split-K path,
+ * decode_attn_gqa_sk_fast.cu:95-112, is fp16 only).
+ */
+int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const void* Ks, const void* Vs,
+                           float* m_part, float* l_part, float* o_part, void* o, int64_t Hq,
+                           int64_t Hkv, int64_t N, int64_t D, int kv_format, int64_t S, int64_t W,
+                           int64_t CW, void* stream);
+
+/*
  * Same as fqkv_gqa_sk_fast, additionally recording the hipEvent_t handles
  * ev_begin / ev_end on `stream` immediately before and after the partial
  * kernel, so a caller can time that kernel alone. Either event may be NULL.
@@ -138,6 +167,22 @@ int fqkv_gqa_sk_fast_timed(const void* q, const void* K, const void* V, float* m
  */
 int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, int64_t D,
                     int kv_format, int path, void* stream);
+
+/*
+ * Per-token symmetric KV quantizer on the GPU, the producer of the int8 / int4
+ * formats above: X [tokens, D] fp16 (x_dtype FQKV_SRC_F16) or fp32
+ * (FQKV_SRC_F32) -> Q [tokens, D] int8 (kv_format FQKV_KV_I8, scale =
+ * max|x|/127) or [tokens, D/2] uint8 packed low nibble first (FQKV_KV_I4,
+ * scale = max|x|/7), scales [tokens] fp16. Bytes identical to the reference's
+ * PyTorch expressions evaluated in X's dtype: round-half-even, clamp to
+ * [-qmax, qmax], scale clamped to >= 1e-8 (tests/test_kernels.py:32-34,
+ * nb:292-299). Alignment: X 16 bytes (8 for fp16 at D = 64), Q 8 / 4 / 2 bytes
+ * (int8 D 128 / int8 D 64 or int4 D 128 / int4 D 64), scales 2 bytes.
+ * Replaces the PyTorch quantizers qpt (tests/test_kernels.py:32-34) and
+ * quant_int4_per_token (nb:292-299), which run on the CPU in the reference.
+ */
+int fqkv_quantize_kv(const void* X, int x_dtype, void* Q, void* scales, int64_t tokens, int64_t D,
+                     int kv_format, void* stream);
 
 /*
  * Split merge mode for calls that split the sequence (gqa_sk_fast with S > 1

@@ -5,15 +5,27 @@ on the input dtype: on an fp16 tensor every elementwise op is evaluated in fp32
 and rounded back to fp16; on an fp32 tensor the ops are plain fp32. The
 restatement follows the same dtype rule, so it reproduces the reference's
 bytes for both the reference tests' fp16 draws and fp32 draws.
+
+The reference runs its quantizers on CUDA tensors (tests/test_kernels.py:27-33,
+``dev="cuda"``). There PyTorch evaluates ``a / 127.0`` -- a tensor divided by
+a Python scalar -- as ``a * fp32(1/127)`` (its CUDA true-division kernel
+multiplies by the reciprocal of a CPU scalar), while ``X / s`` -- tensor by
+tensor -- is a true division. The restatement follows that arithmetic, which
+also makes it device-independent: ``a * (1/qmax)`` rounds the same on CPU.
 """
 
 import numpy as np
 
 
+def _recip(qmax):
+    """fp32(1/qmax): the multiplier PyTorch uses for ``tensor / qmax``."""
+    return np.float32(1.0) / np.float32(qmax)
+
+
 def _per_token(X, qmax):
     """Shared body of the int8 and int4 quantizers.
 
-    a = max|x| over the last axis; s = max(a/qmax, 1e-8); q = round(x/s)
+    a = max|x| over the last axis; s = max(a * fp32(1/qmax), 1e-8); q = round(x/s)
     (round-half-even, ``torch.round``) clamped to [-qmax, qmax]; the stored
     scale is ``s.half()``. tests/test_kernels.py:32-34 (qmax=127),
     nb:292-295 (qmax=7).
@@ -26,7 +38,7 @@ def _per_token(X, qmax):
     X = np.asarray(X)
     if X.dtype == np.float16:
         a = np.abs(X).max(axis=-1, keepdims=True)
-        s = (a.astype(np.float32) / np.float32(qmax)).astype(np.float16)
+        s = (a.astype(np.float32) * _recip(qmax)).astype(np.float16)
         s = np.maximum(s.astype(np.float32), np.float32(1e-8)).astype(np.float16)
         s32 = s.astype(np.float32)
         with np.errstate(divide="ignore", invalid="ignore"):
@@ -35,7 +47,7 @@ def _per_token(X, qmax):
         scale16 = s
     elif X.dtype == np.float32:
         a = np.abs(X).max(axis=-1, keepdims=True)
-        s = np.maximum(a / np.float32(qmax), np.float32(1e-8)).astype(np.float32)
+        s = np.maximum(a * _recip(qmax), np.float32(1e-8)).astype(np.float32)
         quot = (X / s).astype(np.float32)
         scale16 = s.astype(np.float16)
     else:

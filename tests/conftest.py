@@ -25,3 +25,13 @@ def pytest_collection_modifyitems(config, items):
     for item in items:
         if "gpu" in item.keywords:
             item.add_marker(skip)
+
+
+@pytest.fixture(params=["fused", "two_kernel"])
+def merge_mode(request):
+    """Split merge inside the partial kernel (default) or as a separate combine kernel."""
+    import fqkv_decode as fq
+
+    fq._ext._set_two_kernel_merge(request.param == "two_kernel")
+    yield request.param
+    fq._ext._set_two_kernel_merge(False)

@@ -128,3 +128,36 @@ def test_binding_rejects_cpu_tensors():
     mp = torch.zeros(1, 4)
     with pytest.raises(RuntimeError, match="^cuda"):
         fqkv_decode.gqa_sk_fast(q, K, K, mp, mp, torch.zeros(1, 4, 64), q.clone(), 4, 8, 4)
+
+
+def test_capi_quantizer_rejects_bad_args(lib):
+    f = lib.fqkv_quantize_kv
+    f.argtypes = [VP, ctypes.c_int, VP, VP, I64, I64, ctypes.c_int, VP]
+    assert f(16, 0, 16, 16, 4, 128, 0, None) == 1 and "kv_format" in _err(lib)
+    assert f(16, 2, 16, 16, 4, 128, 1, None) == 1 and "x_dtype" in _err(lib)
+    assert f(16, 1, 16, 16, 4, 96, 1, None) == 1 and _err(lib).startswith("D:")
+    assert f(16, 1, 16, 16, 0, 128, 1, None) == 1 and _err(lib).startswith("tokens")
+    assert f(None, 1, 16, 16, 4, 128, 1, None) == 1 and "null" in _err(lib)
+    assert f(24, 1, 16, 16, 4, 128, 1, None) == 1 and "aligned" in _err(lib)
+    assert f(16, 1, 20, 16, 4, 128, 1, None) == 1 and "aligned" in _err(lib)
+
+
+def test_capi_quantized_gqa_and_split_reject_bad_args(lib):
+    fg = lib.fqkv_decode_attn_gqa_quant
+    fg.argtypes = [VP] * 6 + [I64] * 5 + [ctypes.c_int, I64, VP, ctypes.c_size_t, VP]
+    assert fg(16, 16, 16, 16, 16, 16, 1, 32, 8, 64, 128, 0, 8, None, 0, None) == 1 and "kv_format" in _err(lib)
+    assert fg(16, 16, 16, 16, 16, 16, 1, 30, 8, 64, 128, 1, 8, None, 0, None) == 1 and _err(lib).startswith("heads:")
+    assert fg(16, 16, 16, None, 16, 16, 1, 32, 8, 64, 128, 2, 8, None, 0, None) == 1 and "null" in _err(lib)
+    fs = lib.fqkv_gqa_sk_fast_quant
+    fs.argtypes = [VP] * 9 + [I64] * 4 + [ctypes.c_int, I64, I64, I64, VP]
+    assert fs(*[16] * 9, 32, 8, 64, 128, 1, 16, 8, 3, None) == 1 and _err(lib).startswith("CW:")
+    assert fs(*[16] * 9, 32, 8, 64, 128, 0, 16, 8, 4, None) == 1 and "kv_format" in _err(lib)
+    assert fs(*[16] * 9, 32, 8, 64, 128, 2, 0, 8, 4, None) == 1 and _err(lib).startswith("S:")
+
+
+def test_binding_exposes_quantized_and_quantizer_entry_points():
+    for name in ("decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8", "gqa_sk_fast_int4",
+                 "quantize_int8_per_token", "quantize_int4_per_token"):
+        assert callable(getattr(fqkv_decode, name))
+    with pytest.raises(RuntimeError, match="^cuda"):
+        fqkv_decode.quantize_int8_per_token(torch.zeros(4, 128))

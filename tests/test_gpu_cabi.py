@@ -35,6 +35,9 @@ def lib():
     L.fqkv_decode_attn_gqa.argtypes = [VP] * 4 + [I64] * 6 + [VP, SZ, VP]
     L.fqkv_gqa_sk_fast.argtypes = [VP] * 7 + [I64] * 7 + [VP]
     L.fqkv_dequant_kv.argtypes = [VP, VP, VP, I64, I64, ctypes.c_int, ctypes.c_int, VP]
+    L.fqkv_quantize_kv.argtypes = [VP, ctypes.c_int, VP, VP, I64, I64, ctypes.c_int, VP]
+    L.fqkv_decode_attn_gqa_quant.argtypes = [VP] * 6 + [I64] * 5 + [ctypes.c_int, I64, VP, SZ, VP]
+    L.fqkv_gqa_sk_fast_quant.argtypes = [VP] * 9 + [I64] * 4 + [ctypes.c_int, I64, I64, I64, VP]
     return L
 
 
@@ -151,3 +154,49 @@ def test_cabi_dequant_bit_exact(lib, fmt, D, path):
     check(lib, lib.fqkv_dequant_kv(Kd.data_ptr(), Sd.data_ptr(), out.data_ptr(), T, D, fmt, path, stream()))
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("fmt", [KV_I8, KV_I4])
+@pytest.mark.parametrize("src", [0, 1])
+def test_cabi_quantizer_bit_exact(lib, fmt, src):
+    g = torch.Generator().manual_seed(25)
+    T, D = 999, 128
+    X = draw(g, T, D).to(torch.float16 if src == 0 else torch.float32)
+    Xd = X.cuda()
+    Q = torch.empty(T, D if fmt == KV_I8 else D // 2, dtype=torch.int8 if fmt == KV_I8 else torch.uint8,
+                    device="cuda")
+    S = torch.empty(T, dtype=torch.float16, device="cuda")
+    check(lib, lib.fqkv_quantize_kv(Xd.data_ptr(), src, Q.data_ptr(), S.data_ptr(), T, D, fmt, stream()))
+    torch.cuda.synchronize()
+    oq, os_ = (oracle.quant_int8_per_token if fmt == KV_I8 else oracle.quant_int4_per_token)(X.numpy())
+    assert np.array_equal(Q.cpu().numpy(), oq)
+    assert np.array_equal(S.cpu().numpy().view(np.uint16), os_.view(np.uint16))
+
+
+@pytest.mark.parametrize("fmt", [KV_I8, KV_I4])
+def test_cabi_quantized_gqa_and_split(lib, fmt):
+    g = torch.Generator().manual_seed(26)
+    B, Hq, Hkv, N, D, S = 1, 32, 8, 3000, 128, 16
+    q = draw(g, B, Hq, D).half()
+    Kx, Vx = draw(g, B, Hkv, N, D), draw(g, B, Hkv, N, D)
+    if fmt == KV_I8:
+        (Kq, Ks), (Vq, Vs) = quant.quant_int8_per_token(Kx), quant.quant_int8_per_token(Vx)
+        Kf, Vf = quant.dequant_int8(Kq, Ks), quant.dequant_int8(Vq, Vs)
+    else:
+        (Kq, Ks), (Vq, Vs) = quant.quant_int4_per_token(Kx), quant.quant_int4_per_token(Vx)
+        Kf, Vf = quant.dequant_int4(Kq, Ks), quant.dequant_int4(Vq, Vs)
+    ref = oracle.gqa_attention(q.numpy(), Kf.numpy(), Vf.numpy())
+    d = [t.cuda() for t in (q, Kq, Vq, Ks, Vs)]
+    ws, n = workspace(lib, B * Hkv, Hq // Hkv, N, D, fmt, 8)
+    o = torch.empty(B, Hq, D, dtype=torch.float16, device="cuda")
+    check(lib, lib.fqkv_decode_attn_gqa_quant(*[t.data_ptr() for t in d], o.data_ptr(), B, Hq, Hkv, N, D, fmt, 8,
+                                              ws.data_ptr(), n, stream()))
+    mp = torch.empty(Hq, S, device="cuda")
+    lp = torch.empty(Hq, S, device="cuda")
+    op = torch.empty(Hq, S, D, device="cuda")
+    o2 = torch.empty(Hq, D, dtype=torch.float16, device="cuda")
+    check(lib, lib.fqkv_gqa_sk_fast_quant(*[t.data_ptr() for t in d], mp.data_ptr(), lp.data_ptr(), op.data_ptr(),
+                                          o2.data_ptr(), Hq, Hkv, N, D, fmt, S, 8, 8, stream()))
+    torch.cuda.synchronize()
+    assert maxerr(o, ref) <= TOL
+    assert maxerr(o2, ref[0]) <= TOL

@@ -184,14 +184,6 @@ def test_gqa_equals_repeat_kv_plus_mha():
 
 # --------------------------------------------------------------- split-K ----
 
-@pytest.fixture(params=["fused", "two_kernel"])
-def merge_mode(request):
-    """Split merge inside the partial kernel (default) or as a separate combine kernel."""
-    fq._ext._set_two_kernel_merge(request.param == "two_kernel")
-    yield request.param
-    fq._ext._set_two_kernel_merge(False)
-
-
 def run_sk(q, K, V, S, W, CW):
     Hq, D = q.shape
     mp = torch.full((Hq, S), float("nan"), device=DEV)

@@ -1,0 +1,100 @@
+"""The on-GPU per-token KV quantizers (fqkv_quantize_kv) against the oracle's
+restatement of the reference quantizers (tests/test_kernels.py:32-34,
+nb:292-299): bytes and fp16 scales identical, for fp16 and fp32 inputs, both
+head dims, random rows and hand-built edge rows (round-half-even ties,
+all-zero rows, fp16 scale underflow, +-0, single spikes), then the quantized
+cache through the decode kernels."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import fqkv_decode as fq
+from fqkv_decode import quant
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def edge_rows(D, dtype):
+    rows = []
+    r = np.zeros(D, np.float32)
+    rows.append(r.copy())                                   # all zero
+    r = np.zeros(D, np.float32); r[0] = 127.0; r[1:8] = [2.5, -2.5, 3.5, -0.5, 0.5, 1.5, -1.5]
+    rows.append(r)                                          # s = 1: exact .5 ties
+    r = np.zeros(D, np.float32); r[0] = 7.0; r[1:6] = [2.5, -3.5, 0.5, 6.5, -6.5]
+    rows.append(r)                                          # int4 ties at s = 1
+    r = np.zeros(D, np.float32); r[5] = -3.0
+    rows.append(r)                                          # single spike
+    r = np.full(D, 1e-7, np.float32); r[3] = -2e-7
+    rows.append(r)                                          # tiny: fp16 scale underflows to 0
+    r = np.zeros(D, np.float32); r[0] = -0.0; r[1] = 60000.0 if dtype == np.float16 else 3.0e5 / 7.0
+    rows.append(r)                                          # -0 and a huge value
+    r = np.linspace(-1, 1, D).astype(np.float32)
+    rows.append(r)
+    return np.stack(rows).astype(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_gpu_quantizer_bit_exact(dtype, D, fmt):
+    g = torch.Generator().manual_seed(30)
+    X = torch.randn(3, 1000, D, generator=g).to(dtype)
+    X = torch.cat([X.reshape(-1, D), torch.from_numpy(edge_rows(D, X.numpy().dtype))]).contiguous()
+    if fmt == "int8":
+        q, s = fq.quantize_int8_per_token(X.cuda())
+        oq, os_ = oracle.quant_int8_per_token(X.numpy())
+    else:
+        q, s = fq.quantize_int4_per_token(X.cuda())
+        oq, os_ = oracle.quant_int4_per_token(X.numpy())
+    assert q.shape == oq.shape and s.shape == os_.shape
+    np.testing.assert_array_equal(q.cpu().numpy(), oq)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint16), os_.view(np.uint16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_gpu_quantizer_matches_pytorch_expressions_on_gpu(dtype):
+    """Same bytes as the package's PyTorch quantizers evaluated on the same device."""
+    g = torch.Generator().manual_seed(31)
+    X = torch.randn(4, 8, 333, 128, generator=g).to(dtype).cuda()
+    q, s = fq.quantize_int8_per_token(X)
+    tq, ts = quant.quant_int8_per_token(X)
+    assert torch.equal(q, tq) and torch.equal(s.view(torch.int16), ts.view(torch.int16))
+    P, s4 = fq.quantize_int4_per_token(X)
+    tP, ts4 = quant.quant_int4_per_token(X)
+    assert torch.equal(P, tP) and torch.equal(s4.view(torch.int16), ts4.view(torch.int16))
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_gpu_quantized_cache_decodes(fmt):
+    """Quantize K/V on the GPU, decode with the int8 / int4 kernels: within 2e-3
+    of the float64 oracle on the dequantised cache."""
+    g = torch.Generator().manual_seed(32)
+    B, N, D = 16, 2048, 128
+    q = torch.randn(B, D, generator=g).half()
+    K, V = torch.randn(B, N, D, generator=g), torch.randn(B, N, D, generator=g)
+    f = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+    Kq, Ks = f(K.cuda())
+    Vq, Vs = f(V.cuda())
+    if fmt == "int8":
+        out = fq.decode_attn_int8_mw(q.cuda(), Kq, Vq, Ks, Vs, 8)
+        Kf = oracle.dequant_int8(Kq.cpu().numpy(), Ks.cpu().numpy())
+        Vf = oracle.dequant_int8(Vq.cpu().numpy(), Vs.cpu().numpy())
+    else:
+        out = fq.decode_attn_int4(q.cuda(), Kq, Vq, Ks, Vs, 8)
+        Kf = oracle.dequant_int4(Kq.cpu().numpy(), Ks.cpu().numpy())
+        Vf = oracle.dequant_int4(Vq.cpu().numpy(), Vs.cpu().numpy())
+    ref = oracle.attention(q.numpy(), Kf, Vf)
+    assert float(np.abs(out.float().cpu().numpy() - ref).max()) <= TOL
+
+
+def test_gpu_quantizer_rejects_bad_input():
+    with pytest.raises(RuntimeError, match="^D:"):
+        fq.quantize_int8_per_token(torch.zeros(4, 96, device="cuda"))
+    with pytest.raises(RuntimeError, match="^fp16:"):
+        fq.quantize_int4_per_token(torch.zeros(4, 64, device="cuda", dtype=torch.float64))
+    with pytest.raises(RuntimeError, match="^contig:"):
+        fq.quantize_int8_per_token(torch.zeros(64, 4, device="cuda").t())

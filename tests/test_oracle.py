@@ -211,9 +211,12 @@ def test_combine_is_invariant_to_split_order_and_shift():
 # ------------------------------------------------------------ quantizers ----
 
 def _torch_quant(X, qmax):
-    """The reference quantizer expression, evaluated by PyTorch on CPU tensors."""
+    """The reference quantizer expression as PyTorch evaluates it on the reference's CUDA
+    tensors (tests/test_kernels.py:27-33): ``a / qmax`` (tensor by Python scalar) is a
+    multiplication by fp32(1/qmax) there, ``X / s`` a true division. Evaluated here by
+    PyTorch on CPU tensors with the multiplication written out."""
     a = X.abs().amax(-1, keepdim=True)
-    s = (a / float(qmax)).clamp(min=1e-8)
+    s = (a * (1.0 / float(qmax))).clamp(min=1e-8)
     return torch.clamp(torch.round(X / s), -qmax, qmax).to(torch.int8), s.squeeze(-1).half()
 
 
