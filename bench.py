@@ -388,12 +388,141 @@ def suite_mha_small(torch, fq, steps, warmup, rows):
     log("mha_fp16  B=%d N=%d D=%d  %8.2f us  %7.1f GB/s  err %.2e" % (B, N, Dm, ms * 1e3, nbytes / ms / 1e6, err))
 
 
+def suite_splitk_quant(torch, fq, steps, warmup, rows):
+    """gqa_sk_fast_int8 / _int4 (Hq 32, Hkv 8, D 128) at N 16384 (batch 1) and B 8, N 32768:
+    long-context decode over a quantized cache, best of a small S/W sweep."""
+    Hq, Hkv, Dd = 32, 8, 128
+    G = Hq // Hkv
+    for B, N in ((1, 16384), (8, 32768)):
+        for fmt in ("int8", "int4"):
+            g = torch.Generator(device="cuda").manual_seed(5)
+            quantize = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+            per = (2 * B * Hkv * N * Dd if fmt == "int8" else B * Hkv * N * Dd) + 4 * B * Hkv * N
+            ns = _nsets(per)
+            q = torch.randn(B * Hq, Dd, device="cuda", generator=g).half()
+            sets = []
+            for _ in range(ns):
+                Kq, Ks = quantize(torch.randn(B * Hkv, N, Dd, device="cuda", generator=g))
+                Vq, Vs = quantize(torch.randn(B * Hkv, N, Dd, device="cuda", generator=g))
+                sets.append((Kq, Vq, Ks, Vs))
+            Kq, Vq, Ks, Vs = sets[0]
+            if fmt == "int8":
+                Kf, Vf = Kq.float() * Ks.float()[..., None], Vq.float() * Vs.float()[..., None]
+            else:
+                from fqkv_decode import quant
+                Kf, Vf = quant.dequant_int4(Kq, Ks), quant.dequant_int4(Vq, Vs)
+            ref = _ref_mha(torch, q, Kf.repeat_interleave(G, 0), Vf.repeat_interleave(G, 0))
+            del Kf, Vf
+            f = fq.gqa_sk_fast_int8 if fmt == "int8" else fq.gqa_sk_fast_int4
+            nbytes = B * ((2 * Hkv * N * Dd if fmt == "int8" else Hkv * N * Dd) + 4 * Hkv * N + 4 * Hq * Dd)
+            best = None
+            for S in ((16, 32, 64) if B == 1 else (4, 8, 16)):
+                for W in (4, 8):
+                    mp = torch.empty(B * Hq, S, device="cuda")
+                    lp = torch.empty(B * Hq, S, device="cuda")
+                    op = torch.empty(B * Hq, S, Dd, device="cuda")
+                    o = torch.empty(B * Hq, Dd, device="cuda", dtype=torch.float16)
+                    fn = lambda i: f(q, sets[i][0], sets[i][1], sets[i][2], sets[i][3], mp, lp, op, o, S, W, 8)
+                    fn(0)
+                    err = float((o.float() - ref).abs().max())
+                    if err > 2e-3:
+                        log("split-K %s B=%d N=%d S%d W%d failed the gate: %.2e" % (fmt, B, N, S, W, err))
+                        continue
+                    ms = _loop_ms(torch, fn, ns, max(50, steps // 4), max(10, warmup // 4))
+                    if best is None or ms < best[0]:
+                        best = (ms, S, W, err)
+            ms, S, W, err = best
+            rows.append(_row("gqa_sk_fast_" + fmt, {"B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": Dd, "S": S, "W": W,
+                                                    "CW": 8, "sets": ns}, ms, nbytes, err))
+            log("split-K %s B=%d N=%-6d S%-3d W%d  %8.2f us  %7.1f GB/s  err %.2e" % (fmt, B, N, S, W, ms * 1e3,
+                                                                                 nbytes / ms / 1e6, err))
+            del sets, ref
+            torch.cuda.empty_cache()
+
+
+def suite_llama(torch, fq, rows):
+    """End-to-end decode on a random-init Llama-3.2-1B-shaped model (16 layers, 32/8 heads,
+    head_dim 64, hidden 2048, fp16) through transformers, SDPA vs the kernel hook
+    (the reference's nb:1037-1123 measurements: generate tok/s at prompt 512 + 128 new
+    tokens, and the median single decode step at a fixed cache length)."""
+    import time
+
+    import transformers
+    from fqkv_decode import hf_llama
+
+    name = hf_llama.register()
+    cfg = transformers.LlamaConfig(vocab_size=128256, hidden_size=2048, intermediate_size=8192,
+                                   num_hidden_layers=16, num_attention_heads=32, num_key_value_heads=8,
+                                   head_dim=64, max_position_embeddings=8192, attn_implementation="sdpa")
+    torch.manual_seed(0)
+    with torch.device("cuda"):
+        model = transformers.LlamaForCausalLM(cfg).half().eval()
+
+    def set_impl(impl):
+        model.config._attn_implementation = impl
+        for layer in model.model.layers:
+            layer.self_attn.config._attn_implementation = impl
+
+    def tok_per_s(impl, prompt_len=512, gen=128, reps=3):
+        set_impl(impl)
+        ids = torch.randint(0, cfg.vocab_size, (1, prompt_len), device="cuda")
+        best = 1e9
+        with torch.no_grad():
+            model.generate(ids, max_new_tokens=8, min_new_tokens=8, do_sample=False)
+            torch.cuda.synchronize()
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                model.generate(ids, max_new_tokens=gen, min_new_tokens=gen, do_sample=False)
+                torch.cuda.synchronize()
+                best = min(best, time.perf_counter() - t0)
+        return gen / best
+
+    def decode_ms(impl, ctx, reps=100):
+        set_impl(impl)
+        with torch.no_grad():
+            ids = torch.randint(0, cfg.vocab_size, (1, ctx), device="cuda")
+            out = model(ids, use_cache=True)
+            past = out.past_key_values
+            step = torch.randint(0, cfg.vocab_size, (1, 1), device="cuda")
+            ts = []
+            for i in range(reps + 10):
+                past.crop(ctx)
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                model(step, past_key_values=past, use_cache=True)
+                b.record()
+                torch.cuda.synchronize()
+                if i >= 10:
+                    ts.append(a.elapsed_time(b))
+        ts.sort()
+        return ts[len(ts) // 2]
+
+    r = {"bench": "llama_decode", "config": {"model": "random-init LlamaConfig 16L 2048h 32q/8kv hd64 fp16",
+                                             "prompt": 512, "new_tokens": 128}}
+    r["sdpa_tok_s"] = round(tok_per_s("sdpa"), 2)
+    r["kernel_tok_s"] = round(tok_per_s(name), 2)
+    for ctx in (512, 2048, 8192):
+        r["decode_ms_sdpa_ctx%d" % ctx] = round(decode_ms("sdpa", ctx), 4)
+        r["decode_ms_kernel_ctx%d" % ctx] = round(decode_ms(name, ctx), 4)
+    rows.append(r)
+    log("llama     generate tok/s: sdpa %.2f, kernel %.2f; decode step ms (sdpa/kernel) ctx512 %.3f/%.3f "
+        "ctx2048 %.3f/%.3f ctx8192 %.3f/%.3f" % (r["sdpa_tok_s"], r["kernel_tok_s"], r["decode_ms_sdpa_ctx512"],
+                                                 r["decode_ms_kernel_ctx512"], r["decode_ms_sdpa_ctx2048"],
+                                                 r["decode_ms_kernel_ctx2048"], r["decode_ms_sdpa_ctx8192"],
+                                                 r["decode_ms_kernel_ctx8192"]))
+    set_impl("sdpa")
+    del model
+    torch.cuda.empty_cache()
+
+
 def run_suite(torch, fq, path, steps=400, warmup=40):
     rows = []
     suite_mha_small(torch, fq, steps, warmup, rows)
     suite_mha_quant(torch, fq, steps, warmup, rows)
     suite_gqa(torch, fq, steps, warmup, rows)
     suite_splitk(torch, fq, steps, warmup, rows)
+    suite_splitk_quant(torch, fq, steps, warmup, rows)
+    suite_llama(torch, fq, rows)
     with open(path, "w") as f:
         for r in rows:
             f.write(json.dumps(r) + "\n")
