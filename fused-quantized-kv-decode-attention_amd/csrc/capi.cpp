@@ -108,9 +108,21 @@ int check_common(int64_t N, int64_t D, int64_t W) {
 
 // Single-block style decode: rows KV rows, G query heads per row. Splits the
 // sequence internally when rows alone cannot fill the GPU and the workspace allows.
+int64_t row_bytes_of(int fmt, int64_t D) { return fmt == KV_F16 ? 2 * D : (fmt == KV_I8 ? D : D / 2); }
+
+// KV layout of a single-block call (null: the reference's contiguous layout).
+struct Layout {
+  int64_t hkv;
+  int64_t kv_bs, kv_hs, kv_ts;
+  int64_t sc_bs, sc_hs, sc_ts;
+  const int* page_table;
+  const int* seq_lens;
+  int64_t max_pages, page_log2, num_pages;
+};
+
 int run_decode(int fmt, const void* q, const void* K, const void* V, const void* Ks,
                const void* Vs, void* o, int64_t rows, int64_t G, int64_t N, int64_t D, int64_t W,
-               void* ws, size_t ws_bytes, hipStream_t st) {
+               void* ws, size_t ws_bytes, hipStream_t st, const Layout* L = nullptr) {
   int cus = 0;
   int rc = device_cus(&cus);
   if (rc) return rc;
@@ -138,11 +150,27 @@ int run_decode(int fmt, const void* q, const void* K, const void* V, const void*
   p.N = (int)N;
   p.S = (int)S;
   p.chunk = (int)((N + S - 1) / S);
+  if (L && L->page_table) p.chunk = (p.chunk + 15) & ~15;  // a paged tile must not cross a page
   p.ngroups = (int)ngroups;
   p.scale = 1.0f / sqrtf((float)D);
   p.c = p.scale * 1.4426950408889634f;
   p.direct = S == 1;
   p.slot = -1;
+  set_contiguous_layout(p, rows, N, (int)row_bytes_of(fmt, D));
+  if (L) {
+    p.hkv = (int)L->hkv;
+    p.kv_bs = L->kv_bs;
+    p.kv_hs = L->kv_hs;
+    p.kv_ts = (int)L->kv_ts;
+    p.sc_bs = L->sc_bs;
+    p.sc_hs = L->sc_hs;
+    p.sc_ts = (int)L->sc_ts;
+    p.page_table = L->page_table;
+    p.seq_lens = L->seq_lens;
+    p.max_pages = (int)L->max_pages;
+    p.page_log2 = (int)L->page_log2;
+    p.num_pages = (int)L->num_pages;
+  }
   if (!p.direct) {
     float* f = (float*)ws;
     p.m_part = f;
@@ -177,8 +205,10 @@ int check_ptrs_quant(int fmt, int64_t D, const void* q, const void* K, const voi
 }
 
 // The kernels address a KV row block with 32-bit byte offsets.
+int64_t row_bytes_of(int fmt, int64_t D);
+
 int check_span(int64_t N, int64_t D, int fmt) {
-  const int64_t row_bytes = fmt == KV_F16 ? 2 * D : (fmt == KV_I8 ? D : D / 2);
+  const int64_t row_bytes = row_bytes_of(fmt, D);
   if (N * row_bytes > (int64_t)UINT32_MAX)
     return fail(FQKV_ERR_ARG, "N: %lld tokens of %lld bytes exceed the 4 GiB per-row span", (long long)N,
                 (long long)row_bytes);
@@ -228,6 +258,7 @@ int sk_fast(int fmt, const void* q, const void* K, const void* V, const void* Ks
   p.c = p.scale * 1.4426950408889634f;
   p.o = (_Float16*)o;
   p.direct = 0;
+  set_contiguous_layout(p, Hkv, N, (int)row_bytes_of(fmt, D));
   // S == 1 still writes the scratch (the caller asked for it); one split needs
   // no merge beyond the workgroup's own, done by the two-kernel path's combine.
   p.slot = S > 1 ? merge_slot(Hkv * ngroups) : -1;
@@ -364,6 +395,79 @@ int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const vo
     return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
   return sk_fast(kv_format, q, K, V, Ks, Vs, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW, stream,
                  nullptr, nullptr);
+}
+
+static int check_layout_common(int fmt, int64_t D, const void* q, const void* K, const void* V,
+                               const void* Ks, const void* Vs, const void* o, int64_t kv_bs, int64_t kv_hs,
+                               int64_t kv_ts, int64_t sc_bs, int64_t sc_hs, int64_t sc_ts) {
+  if (fmt != FQKV_KV_F16 && fmt != FQKV_KV_I8 && fmt != FQKV_KV_I4)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_F16, FQKV_KV_I8 or FQKV_KV_I4");
+  int rc = fmt == KV_F16 ? check_ptrs_kv(q, K, V, o) : check_ptrs_quant(fmt, D, q, K, V, Ks, Vs, o);
+  if (rc) return rc;
+  const int64_t rb = row_bytes_of(fmt, D);
+  const int64_t al = (fmt == KV_I4 && D == 64) ? 8 : 16;
+  if (kv_ts < rb || kv_ts > INT_MAX || kv_ts % al || kv_hs < 0 || kv_hs % al || kv_bs < 0 || kv_bs % al)
+    return fail(FQKV_ERR_ARG, "strides: KV token stride must be >= %lld bytes and all KV strides multiples of %lld "
+                "bytes, got batch %lld, head %lld, token %lld", (long long)rb, (long long)al, (long long)kv_bs,
+                (long long)kv_hs, (long long)kv_ts);
+  if (fmt != KV_F16 && (sc_ts < 1 || sc_ts > INT_MAX / 2 || sc_hs < 0 || sc_bs < 0))
+    return fail(FQKV_ERR_ARG, "strides: scale strides must be non-negative with a token stride >= 1");
+  return FQKV_OK;
+}
+
+int fqkv_decode_attn_gqa_strided(const void* q, const void* K, const void* V, const void* Ks, const void* Vs,
+                                 void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int kv_format,
+                                 int64_t kv_batch_stride, int64_t kv_head_stride, int64_t kv_token_stride,
+                                 int64_t sc_batch_stride, int64_t sc_head_stride, int64_t sc_token_stride,
+                                 int64_t W, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_common(N, D, W);
+  if (rc) return rc;
+  if (B < 1) return fail(FQKV_ERR_ARG, "B: batch must be >= 1, got %lld", (long long)B);
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
+    return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
+  if ((rc = check_layout_common(kv_format, D, q, K, V, Ks, Vs, o, kv_batch_stride, kv_head_stride,
+                                kv_token_stride, sc_batch_stride, sc_head_stride, sc_token_stride)))
+    return rc;
+  if (N * kv_token_stride > (int64_t)UINT32_MAX || (kv_format != KV_F16 && 2 * N * sc_token_stride > (int64_t)UINT32_MAX))
+    return fail(FQKV_ERR_ARG, "N: %lld tokens at a %lld-byte stride exceed the 4 GiB per-row span", (long long)N,
+                (long long)kv_token_stride);
+  Layout L{Hkv, kv_batch_stride, kv_head_stride, kv_token_stride, sc_batch_stride, sc_head_stride, sc_token_stride,
+           nullptr, nullptr, 0, 0, 0};
+  return run_decode(kv_format, q, K, V, Ks, Vs, o, B * Hkv, Hq / Hkv, N, D, W, workspace, workspace_bytes,
+                    (hipStream_t)stream, &L);
+}
+
+int fqkv_decode_attn_gqa_paged(const void* q, const void* K_pages, const void* V_pages, const void* Ks_pages,
+                               const void* Vs_pages, const int32_t* page_table, const int32_t* seq_lens, void* o,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t num_pages, int64_t max_pages,
+                               int64_t page_size, int64_t max_seq_len, int64_t D, int kv_format,
+                               int64_t kv_page_stride, int64_t kv_head_stride, int64_t kv_token_stride,
+                               int64_t sc_page_stride, int64_t sc_head_stride, int64_t sc_token_stride,
+                               int64_t W, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_common(max_seq_len, D, W);
+  if (rc) return rc;
+  if (B < 1) return fail(FQKV_ERR_ARG, "B: batch must be >= 1, got %lld", (long long)B);
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
+    return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
+  if (page_size < 16 || page_size > (1 << 20) || (page_size & (page_size - 1)))
+    return fail(FQKV_ERR_ARG, "page_size: must be a power of two in [16, 2^20], got %lld", (long long)page_size);
+  if (num_pages < 1 || num_pages > INT_MAX || max_pages < 1 || max_pages > INT_MAX ||
+      max_pages * page_size > INT_MAX - 1024)
+    return fail(FQKV_ERR_ARG, "pages: need 1 <= num_pages, max_pages and max_pages * page_size < 2^31 - 1024");
+  if (!page_table || !seq_lens) return fail(FQKV_ERR_ARG, "null page table or sequence lengths");
+  if (!aligned(page_table, 4) || !aligned(seq_lens, 4)) return fail(FQKV_ERR_ARG, "page table and lengths must be 4-byte aligned");
+  if ((rc = check_layout_common(kv_format, D, q, K_pages, V_pages, Ks_pages, Vs_pages, o, kv_page_stride,
+                                kv_head_stride, kv_token_stride, sc_page_stride, sc_head_stride, sc_token_stride)))
+    return rc;
+  if (16 * kv_token_stride > (int64_t)UINT32_MAX)
+    return fail(FQKV_ERR_ARG, "strides: token stride too large");
+  int64_t lg = 0;
+  while ((int64_t(1) << lg) < page_size) ++lg;
+  const int64_t N = max_seq_len < max_pages * page_size ? max_seq_len : max_pages * page_size;
+  Layout L{Hkv, kv_page_stride, kv_head_stride, kv_token_stride, sc_page_stride, sc_head_stride, sc_token_stride,
+           page_table, seq_lens, max_pages, lg, num_pages};
+  return run_decode(kv_format, q, K_pages, V_pages, Ks_pages, Vs_pages, o, B * Hkv, Hq / Hkv, N, D, W, workspace,
+                    workspace_bytes, (hipStream_t)stream, &L);
 }
 
 int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, int64_t D,

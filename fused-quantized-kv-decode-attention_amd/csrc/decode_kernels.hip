@@ -273,7 +273,7 @@ __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const f
   }
 }
 
-template <int FMT, int D, int HG>
+template <int FMT, int D, int HG, bool PAGED>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
   using VG = VGeom<F::ROWB, D>;
@@ -297,15 +297,22 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   wg /= p.S;
   const int hg = wg % p.ngroups;
   const int r = wg / p.ngroups;
+  // KV row r = (sequence b, KV head h); its tokens sit kv_ts bytes apart
+  const int b = r / p.hkv;
+  const int h = r - b * p.hkv;
+  const uint32_t ts = (uint32_t)p.kv_ts;
+  int nr = p.N;  // tokens of this row
+  if constexpr (PAGED) nr = min(min(p.seq_lens[b], p.N), p.max_pages << p.page_log2);
   const int lo = s * p.chunk;
-  const int hi = min(lo + p.chunk, p.N);
+  const int hi = min(lo + p.chunk, nr);
   const int hbase = hg * HG;
   const int hcnt = min(HG, p.G - hbase);
   const size_t qrow0 = (size_t)r * p.G + hbase;
-  const uint8_t* Kr = p.K + (size_t)r * p.N * F::ROWB;
-  const uint8_t* Vr = p.V + (size_t)r * p.N * F::ROWB;
-  const _Float16* Ksr = F::QUANT ? p.Ks + (size_t)r * p.N : nullptr;
-  const _Float16* Vsr = F::QUANT ? p.Vs + (size_t)r * p.N : nullptr;
+  // base of the row's token 0 (paged: of the row's head within a page)
+  const uint8_t* Kr = p.K + (PAGED ? 0 : (size_t)b * p.kv_bs) + (size_t)h * p.kv_hs;
+  const uint8_t* Vr = p.V + (PAGED ? 0 : (size_t)b * p.kv_bs) + (size_t)h * p.kv_hs;
+  const _Float16* Ksr = F::QUANT ? p.Ks + (PAGED ? 0 : (size_t)b * p.sc_bs) + (size_t)h * p.sc_hs : nullptr;
+  const _Float16* Vsr = F::QUANT ? p.Vs + (PAGED ? 0 : (size_t)b * p.sc_bs) + (size_t)h * p.sc_hs : nullptr;
 
   const int n = lane & 15;  // query head column of P^T and O^T; token row of the K operand
   const int R = lane >> 4;  // lane row: K dword group; scores and V of tokens 4R .. 4R+3
@@ -328,13 +335,49 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 
   // Buffer descriptors end at the split's last token, so rows past it read
   // as zeros (their scores are masked); offsets are 32-bit from the row block.
-  const uint32_t nbytes = (uint32_t)hi * F::ROWB;
-  const rsrc_t rK = make_rsrc(Kr, nbytes);
-  const rsrc_t rV = make_rsrc(Vr, nbytes);
-  const rsrc_t rKs = make_rsrc(Ksr, 2u * (uint32_t)hi);
-  const rsrc_t rVs = make_rsrc(Vsr, 2u * (uint32_t)hi);
-  const uint32_t koff = (uint32_t)n * F::ROWB + F::klane(R);
-  const uint32_t voff = (uint32_t)R * F::ROWB + (uint32_t)n * VG::VBYTES;
+  // Paged rows get a descriptor per tile instead (a tile never crosses a
+  // page), ending at the tile's last valid token; a tile whose page id is out
+  // of range gets an empty descriptor and its tokens are masked.
+  const uint32_t sts = 2u * (uint32_t)p.sc_ts;  // scale stride in bytes
+  const rsrc_t rK = make_rsrc(Kr, PAGED ? 0u : (uint32_t)hi * ts);
+  const rsrc_t rV = make_rsrc(Vr, PAGED ? 0u : (uint32_t)hi * ts);
+  const rsrc_t rKs = make_rsrc(Ksr, PAGED ? 0u : (uint32_t)hi * sts);
+  const rsrc_t rVs = make_rsrc(Vsr, PAGED ? 0u : (uint32_t)hi * sts);
+  const uint32_t koff = (uint32_t)n * ts + F::klane(R);
+  const uint32_t voff = (uint32_t)R * ts + (uint32_t)n * VG::VBYTES;
+  // tile t's sources: descriptors and the byte offset of its first token
+  struct TileSrc {
+    rsrc_t k, v, ks, vs;
+    uint32_t off, soff;
+    bool ok;
+  };
+  auto tile_src = [&](int tb) -> TileSrc {
+    TileSrc t;
+    if constexpr (PAGED) {
+      const int pg = tb >> p.page_log2;
+      const int pid = (tb < hi) ? p.page_table[(size_t)b * p.max_pages + pg] : -1;
+      t.ok = pid >= 0 && pid < p.num_pages;
+      const int in = tb - (pg << p.page_log2);
+      const uint32_t nrow = t.ok ? (uint32_t)min(16, hi - tb) : 0u;
+      const size_t kvb = (size_t)(t.ok ? pid : 0) * p.kv_bs + (size_t)in * ts;
+      const size_t scb = (size_t)(t.ok ? pid : 0) * p.sc_bs + (size_t)in * p.sc_ts;
+      t.k = make_rsrc(Kr + kvb, nrow * ts);
+      t.v = make_rsrc(Vr + kvb, nrow * ts);
+      t.ks = make_rsrc(F::QUANT ? Ksr + scb : nullptr, nrow * sts);
+      t.vs = make_rsrc(F::QUANT ? Vsr + scb : nullptr, nrow * sts);
+      t.off = 0;
+      t.soff = 0;
+    } else {
+      t.k = rK;
+      t.v = rV;
+      t.ks = rKs;
+      t.vs = rVs;
+      t.off = (uint32_t)tb * ts;
+      t.soff = (uint32_t)tb * sts;
+      t.ok = true;
+    }
+    return t;
+  };
 
   // Each pass covers U tiles of this wave (tiles interleave across waves).
   // All K loads of the pass are issued, then all V loads, before anything is
@@ -349,16 +392,18 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     typename F::KT kr[U][F::KL];
     uint32_t vr[U][4][VD];
     _Float16 ks[U][4], vs[U][4];  // per-token scales of tokens 4R + k (int8 / int4)
+    TileSrc src[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) src[u] = tile_src(pb + u * step);
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int tb = pb + u * step;
-      F::load_k(rK, (uint32_t)tb * F::ROWB + koff, kr[u]);
+      F::load_k(src[u].k, src[u].off + koff, kr[u]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         if constexpr (F::QUANT) {
-          const uint32_t so = 2u * (uint32_t)(tb + 4 * R + k);
-          ks[u][k] = __builtin_bit_cast(_Float16, buf_load<2>(rKs, so));
-          vs[u][k] = __builtin_bit_cast(_Float16, buf_load<2>(rVs, so));
+          const uint32_t so = src[u].soff + (uint32_t)(4 * R + k) * sts;
+          ks[u][k] = __builtin_bit_cast(_Float16, buf_load<2>(src[u].ks, so));
+          vs[u][k] = __builtin_bit_cast(_Float16, buf_load<2>(src[u].vs, so));
         } else {
           ks[u][k] = (_Float16)1.0f;
           vs[u][k] = (_Float16)1.0f;
@@ -367,9 +412,9 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t base = (uint32_t)(pb + u * step) * F::ROWB + voff;
+      const uint32_t base = src[u].off + voff;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) load_vchunk<VG::VBYTES, VD>(rV, base + (uint32_t)(4 * j) * F::ROWB, vr[u][j]);
+      for (int j = 0; j < 4; ++j) load_vchunk<VG::VBYTES, VD>(src[u].v, base + (uint32_t)(4 * j) * ts, vr[u][j]);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
 
@@ -388,7 +433,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     for (int u = 0; u < U; ++u)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const bool ok = pb + u * step + 4 * R + k < hi;
+        const bool ok = src[u].ok && pb + u * step + 4 * R + k < hi;
         x[u][k] = ok ? c4[u][k] * (float)ks[u][k] : -INFINITY;
         mx = fmaxf(mx, x[u][k]);
       }
@@ -551,7 +596,10 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
 // ------------------------------------------------------------ launchers ----
 template <int FMT, int D, int HG>
 static hipError_t launch_partial_t(const PartialParams& p, int nblocks, int nw, hipStream_t st) {
-  hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG>), dim3(nblocks), dim3(64 * nw), 0, st, p);
+  if (p.page_table)
+    hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, true>), dim3(nblocks), dim3(64 * nw), 0, st, p);
+  else
+    hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false>), dim3(nblocks), dim3(64 * nw), 0, st, p);
   return hipGetLastError();
 }
 

@@ -30,7 +30,38 @@ struct PartialParams {
   float scale;           // softmax scale (natural-log units for m_part)
   int direct;            // 1: S == 1, write normalised fp16 output
   int slot;              // !direct: arrival-counter slot for the in-kernel merge, -1 = none
+  // KV layout: row r = (b, h) = (r / hkv, r % hkv) starts at K + b*kv_bs + h*kv_hs
+  // and its tokens are kv_ts bytes apart; scales likewise in elements. Paged
+  // (page_table != null): b indexes page_table [B, max_pages] and seq_lens [B];
+  // kv_bs / sc_bs are then the page strides and token t of row r lies in page
+  // page_table[b][t >> page_log2] at in-page position t & (2^page_log2 - 1).
+  int hkv;
+  int64_t kv_bs, kv_hs;
+  int kv_ts;
+  int64_t sc_bs, sc_hs;
+  int sc_ts;
+  const int* page_table;
+  const int* seq_lens;
+  int max_pages;
+  int page_log2;
+  int num_pages;
 };
+
+// The reference's contiguous layout: K, V [rows, N, row_bytes], scales [rows, N].
+inline void set_contiguous_layout(PartialParams& p, int64_t rows, int64_t N, int row_bytes) {
+  p.hkv = (int)rows;
+  p.kv_bs = 0;
+  p.kv_hs = N * row_bytes;
+  p.kv_ts = row_bytes;
+  p.sc_bs = 0;
+  p.sc_hs = N;
+  p.sc_ts = 1;
+  p.page_table = nullptr;
+  p.seq_lens = nullptr;
+  p.max_pages = 0;
+  p.page_log2 = 0;
+  p.num_pages = 0;
+}
 
 // In-kernel split merge: each call with S > 1 takes one of SPLIT_SLOTS slots
 // of MAX_SPLIT_GROUPS arrival counters (one per (KV row, head group)).

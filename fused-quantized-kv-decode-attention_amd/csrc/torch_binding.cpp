@@ -34,6 +34,14 @@ void check_gpu(std::initializer_list<const torch::Tensor*> ts) {
   }
 }
 
+// Device checks for tensors that may be strided views (paged caches).
+void check_gpu_strided(std::initializer_list<const torch::Tensor*> ts, const torch::Tensor& like) {
+  for (const torch::Tensor* t : ts) {
+    TORCH_CHECK(t->is_cuda(), "cuda: all tensors must be on the GPU");
+    TORCH_CHECK(t->device() == like.device(), "cuda: all tensors must be on the same device");
+  }
+}
+
 void check_half(const torch::Tensor& t, const char* name) {
   TORCH_CHECK(t.scalar_type() == torch::kHalf, "fp16: ", name, " must be float16");
 }
@@ -303,6 +311,121 @@ void gqa_sk_fast_int4(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::
   gqa_sk_fast_quant(FQKV_KV_I4, q, K, V, Ks, Vs, m_part, l_part, o_part, o, S, W, CW);
 }
 
+// ---- other KV layouts (no counterpart in the reference) ----
+
+// KV format from K's dtype; returns FQKV_KV_*, sets D (unpacked head_dim) and the element size.
+int kv_format_of(const torch::Tensor& K, int64_t* D, int64_t* elem) {
+  if (K.scalar_type() == torch::kHalf) {
+    *D = K.size(-1);
+    *elem = 2;
+    return FQKV_KV_F16;
+  }
+  if (K.scalar_type() == torch::kChar) {
+    *D = K.size(-1);
+    *elem = 1;
+    return FQKV_KV_I8;
+  }
+  TORCH_CHECK(K.scalar_type() == torch::kByte, "fp16: K must be float16, int8 or packed uint8 (int4)");
+  *D = 2 * K.size(-1);
+  *elem = 1;
+  return FQKV_KV_I4;
+}
+
+void check_scales(int fmt, const c10::optional<torch::Tensor>& Ks, const c10::optional<torch::Tensor>& Vs,
+                  at::IntArrayRef want) {
+  if (fmt == FQKV_KV_F16) return;
+  TORCH_CHECK(Ks.has_value() && Vs.has_value(), "int8: int8 / int4 K and V need per-token scales Ks and Vs");
+  check_gpu_strided({&*Ks, &*Vs}, *Ks);
+  check_half(*Ks, "Ks");
+  check_half(*Vs, "Vs");
+  TORCH_CHECK(Ks->sizes() == want && Vs->sizes() == want && Ks->strides() == Vs->strides(),
+              "shape: scales must be ", want, " with equal strides; got ", Ks->sizes(), " and ", Vs->sizes());
+}
+
+// decode_attn_gqa_nhd(q[B,Hq,D], K[B,N,Hkv,D or D/2], V, W, Ks=None[B,N,Hkv], Vs=None) -> o[B,Hq,D]:
+// the token-major layout FlashInfer uses (flashinfer_looptimed.py:63-65).
+torch::Tensor decode_attn_gqa_nhd(torch::Tensor q, torch::Tensor K, torch::Tensor V, int64_t W,
+                                  c10::optional<torch::Tensor> Ks, c10::optional<torch::Tensor> Vs) {
+  check_gpu({&q, &K, &V});
+  check_half(q, "q");
+  TORCH_CHECK(q.dim() == 3 && K.dim() == 4 && V.sizes() == K.sizes() && V.scalar_type() == K.scalar_type() &&
+                  q.size(0) == K.size(0),
+              "shape: expected q [B,Hq,D], K and V [B,N,Hkv,D]; got q ", q.sizes(), ", K ", K.sizes());
+  TORCH_CHECK(K.is_contiguous() && V.is_contiguous(), "contig: K and V must be contiguous [B,N,Hkv,D]");
+  int64_t D = 0, elem = 0;
+  const int fmt = kv_format_of(K, &D, &elem);
+  check_D(D);
+  TORCH_CHECK(q.size(2) == D, "shape: q head_dim ", q.size(2), " does not match KV head_dim ", D);
+  const int64_t B = q.size(0), Hq = q.size(1), N = K.size(1), Hkv = K.size(2);
+  check_W(W);
+  TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
+  TORCH_CHECK(N >= 1, "N: need at least one cached token");
+  check_scales(fmt, Ks, Vs, {B, N, Hkv});
+  if (fmt != FQKV_KV_F16) {
+    TORCH_CHECK(Ks->device() == q.device(), "cuda: all tensors must be on the same device");
+    TORCH_CHECK(Ks->is_contiguous() && Vs->is_contiguous(), "contig: scales must be contiguous");
+  }
+  const c10::DeviceGuard guard(q.device());
+  auto o = torch::empty({B, Hq, D}, q.options());
+  auto ws = workspace_for(q, B * Hkv, Hq / Hkv, N, D, fmt, W);
+  const int64_t rb = K.size(3) * elem;
+  check_rc(fqkv_decode_attn_gqa_strided(q.data_ptr(), K.data_ptr(), V.data_ptr(),
+                                        fmt == FQKV_KV_F16 ? nullptr : Ks->data_ptr(),
+                                        fmt == FQKV_KV_F16 ? nullptr : Vs->data_ptr(), o.data_ptr(), B, Hq, Hkv, N, D,
+                                        fmt, N * Hkv * rb, rb, Hkv * rb, N * Hkv, 1, Hkv, W,
+                                        ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0,
+                                        cur_stream(q)),
+           "launch");
+  return o;
+}
+
+// decode_attn_gqa_paged(q[B,Hq,D], K_pages[P,page_size,Hkv,D or D/2], V_pages, page_table[B,max_pages] int32,
+//                       seq_lens[B] int32, max_seq_len, W, Ks_pages=None[P,page_size,Hkv], Vs_pages=None)
+// -> o[B,Hq,D]. The page tensors may be any strided view whose last dim is contiguous, so HND
+// storage [P,Hkv,page_size,D] is passed as its permute(0,2,1,3).
+torch::Tensor decode_attn_gqa_paged(torch::Tensor q, torch::Tensor Kp, torch::Tensor Vp, torch::Tensor page_table,
+                                    torch::Tensor seq_lens, int64_t max_seq_len, int64_t W,
+                                    c10::optional<torch::Tensor> Ks, c10::optional<torch::Tensor> Vs) {
+  check_gpu({&q, &page_table, &seq_lens});
+  check_gpu_strided({&Kp, &Vp}, q);
+  check_half(q, "q");
+  TORCH_CHECK(q.dim() == 3 && Kp.dim() == 4 && Vp.sizes() == Kp.sizes() && Vp.strides() == Kp.strides() &&
+                  Vp.scalar_type() == Kp.scalar_type(),
+              "shape: expected q [B,Hq,D], K_pages and V_pages [P,page_size,Hkv,D] with equal strides; got q ",
+              q.sizes(), ", K_pages ", Kp.sizes());
+  TORCH_CHECK(Kp.stride(3) == 1, "contig: the head_dim axis of the pages must be contiguous");
+  TORCH_CHECK(page_table.scalar_type() == torch::kInt && seq_lens.scalar_type() == torch::kInt,
+              "shape: page_table and seq_lens must be int32");
+  TORCH_CHECK(page_table.dim() == 2 && page_table.is_contiguous() && page_table.size(0) == q.size(0) &&
+                  seq_lens.dim() == 1 && seq_lens.is_contiguous() && seq_lens.size(0) == q.size(0),
+              "shape: expected page_table [B,max_pages] and seq_lens [B], contiguous");
+  int64_t D = 0, elem = 0;
+  const int fmt = kv_format_of(Kp, &D, &elem);
+  check_D(D);
+  TORCH_CHECK(q.size(2) == D, "shape: q head_dim ", q.size(2), " does not match KV head_dim ", D);
+  const int64_t B = q.size(0), Hq = q.size(1), P = Kp.size(0), page = Kp.size(1), Hkv = Kp.size(2);
+  check_W(W);
+  TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
+  TORCH_CHECK(max_seq_len >= 1, "N: max_seq_len must be >= 1");
+  check_scales(fmt, Ks, Vs, {P, page, Hkv});
+  if (fmt != FQKV_KV_F16) TORCH_CHECK(Ks->device() == q.device(), "cuda: all tensors must be on the same device");
+  const c10::DeviceGuard guard(q.device());
+  auto o = torch::empty({B, Hq, D}, q.options());
+  const int64_t max_pages = page_table.size(1);
+  const int64_t N = std::min<int64_t>(max_seq_len, max_pages * page);
+  auto ws = workspace_for(q, B * Hkv, Hq / Hkv, N, D, fmt, W);
+  const bool qz = fmt != FQKV_KV_F16;
+  check_rc(fqkv_decode_attn_gqa_paged(q.data_ptr(), Kp.data_ptr(), Vp.data_ptr(), qz ? Ks->data_ptr() : nullptr,
+                                      qz ? Vs->data_ptr() : nullptr, page_table.data_ptr<int32_t>(),
+                                      seq_lens.data_ptr<int32_t>(), o.data_ptr(), B, Hq, Hkv, P, max_pages, page,
+                                      max_seq_len, D, fmt, Kp.stride(0) * elem, Kp.stride(2) * elem,
+                                      Kp.stride(1) * elem, qz ? Ks->stride(0) : 0, qz ? Ks->stride(2) : 0,
+                                      qz ? Ks->stride(1) : 1, W, ws.defined() ? ws.data_ptr() : nullptr,
+                                      ws.defined() ? ws.numel() : 0, cur_stream(q)),
+           "launch");
+  return o;
+}
+
 // Dequantise int8 [T,D] / int4 [T,D/2] KV through the kernels' conversions.
 torch::Tensor dequant_kv(torch::Tensor Kq, torch::Tensor Ks, int64_t path) {
   check_gpu({&Kq, &Ks});
@@ -394,6 +517,12 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gqa_sk_fast_int4", &gqa_sk_fast_int4, "GQA split-K int4-KV decode", py::arg("q"), py::arg("K"),
         py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("m_part"), py::arg("l_part"), py::arg("o_part"),
         py::arg("o"), py::arg("S"), py::arg("W"), py::arg("CW"));
+  m.def("decode_attn_gqa_nhd", &decode_attn_gqa_nhd, "GQA decode over a token-major [B,N,Hkv,D] KV cache",
+        py::arg("q"), py::arg("K"), py::arg("V"), py::arg("W"), py::arg("Ks") = py::none(),
+        py::arg("Vs") = py::none());
+  m.def("decode_attn_gqa_paged", &decode_attn_gqa_paged, "GQA decode over a paged KV cache", py::arg("q"),
+        py::arg("K_pages"), py::arg("V_pages"), py::arg("page_table"), py::arg("seq_lens"), py::arg("max_seq_len"),
+        py::arg("W"), py::arg("Ks_pages") = py::none(), py::arg("Vs_pages") = py::none());
   m.def("quantize_int8_per_token", &quantize_int8_per_token,
         "per-token int8 KV quantizer on the GPU -> (int8 [..., D], fp16 scales [...])", py::arg("X"));
   m.def("quantize_int4_per_token", &quantize_int4_per_token,

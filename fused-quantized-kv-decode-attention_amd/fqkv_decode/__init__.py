@@ -18,6 +18,10 @@ Beyond the reference (same conventions, no counterpart there):
         m_part, l_part, o_part, o, S, W, CW)        split-K over an int8 / int4 cache
     quantize_int8_per_token / quantize_int4_per_token(X[..., D]) -> (bytes, fp16 scales)
                                                     the KV quantizers as GPU kernels
+    decode_attn_gqa_nhd(q[B,Hq,D], K[B,N,Hkv,D], V, W, Ks=None, Vs=None) -> o[B,Hq,D]
+                                                    token-major (FlashInfer NHD) KV layout
+    decode_attn_gqa_paged(q, K_pages[P,page,Hkv,D], V_pages, page_table[B,max_pages], seq_lens[B],
+        max_seq_len, W, Ks_pages=None, Vs_pages=None) -> o[B,Hq,D]      paged KV cache
 
 Callers of the reference build each kernel with
 ``torch.utils.cpp_extension.load(name=..., sources=["kernels/<file>.cu"], ...)``
@@ -48,6 +52,8 @@ __all__ = [
     "gqa_sk_fast_int4",
     "quantize_int8_per_token",
     "quantize_int4_per_token",
+    "decode_attn_gqa_nhd",
+    "decode_attn_gqa_paged",
     "load",
     "lib_path",
     "ext_path",
@@ -55,7 +61,8 @@ __all__ = [
 
 _ENTRY_POINTS = ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa",
                  "gqa_sk_fast", "decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8",
-                 "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token")
+                 "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token",
+                 "decode_attn_gqa_nhd", "decode_attn_gqa_paged")
 _EXT = None
 
 

@@ -147,6 +147,44 @@ int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const vo
                            int64_t CW, void* stream);
 
 /*
+ * GQA-aware decode over a KV cache in any strided layout (fp16, int8 or int4
+ * per kv_format): KV head h of sequence b starts at
+ * K + b*kv_batch_stride + h*kv_head_stride and its tokens lie kv_token_stride
+ * bytes apart (each token row is D fp16 / D int8 / D/2 packed bytes); scales
+ * likewise in fp16 elements (ignored for fp16). [B, Hkv, N, D] is the
+ * reference layout; [B, N, Hkv, D] (FlashInfer's NHD, flashinfer_looptimed.py:63-65)
+ * has kv_token_stride = Hkv*row_bytes, kv_head_stride = row_bytes,
+ * kv_batch_stride = N*Hkv*row_bytes. q [B, Hq, D], o [B, Hq, D] fp16.
+ * Strides are multiples of 16 bytes (8 for int4 at D = 64); N * kv_token_stride
+ * < 4 GiB. No counterpart in the reference (contiguous [B, Hkv, N, D] only).
+ */
+int fqkv_decode_attn_gqa_strided(const void* q, const void* K, const void* V, const void* Ks, const void* Vs,
+                                 void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int kv_format,
+                                 int64_t kv_batch_stride, int64_t kv_head_stride, int64_t kv_token_stride,
+                                 int64_t sc_batch_stride, int64_t sc_head_stride, int64_t sc_token_stride,
+                                 int64_t W, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * GQA-aware decode over a paged KV cache. Sequence b has seq_lens[b] tokens
+ * (int32, device); its token t lives in page page_table[b*max_pages + t/page_size]
+ * (int32, device) at in-page position t % page_size. Within page pg, KV head h
+ * starts at K_pages + pg*kv_page_stride + h*kv_head_stride, tokens
+ * kv_token_stride bytes apart (NHD pages [num_pages, page_size, Hkv, D] and
+ * HND pages [num_pages, Hkv, page_size, D] are both strides); scales alike in
+ * elements. page_size: a power of two >= 16. max_seq_len bounds every
+ * seq_lens[b] (longer sequences are cut there; the kernel also never reads past
+ * max_pages pages); a page id outside [0, num_pages) contributes nothing.
+ * No counterpart in the reference.
+ */
+int fqkv_decode_attn_gqa_paged(const void* q, const void* K_pages, const void* V_pages, const void* Ks_pages,
+                               const void* Vs_pages, const int32_t* page_table, const int32_t* seq_lens, void* o,
+                               int64_t B, int64_t Hq, int64_t Hkv, int64_t num_pages, int64_t max_pages,
+                               int64_t page_size, int64_t max_seq_len, int64_t D, int kv_format,
+                               int64_t kv_page_stride, int64_t kv_head_stride, int64_t kv_token_stride,
+                               int64_t sc_page_stride, int64_t sc_head_stride, int64_t sc_token_stride,
+                               int64_t W, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Same as fqkv_gqa_sk_fast, additionally recording the hipEvent_t handles
  * ev_begin / ev_end on `stream` immediately before and after the partial
  * kernel, so a caller can time that kernel alone. Either event may be NULL.

@@ -161,3 +161,23 @@ def test_binding_exposes_quantized_and_quantizer_entry_points():
         assert callable(getattr(fqkv_decode, name))
     with pytest.raises(RuntimeError, match="^cuda"):
         fqkv_decode.quantize_int8_per_token(torch.zeros(4, 128))
+
+
+def test_capi_layout_entry_points_reject_bad_args(lib):
+    fs = lib.fqkv_decode_attn_gqa_strided
+    fs.argtypes = [VP] * 6 + [I64] * 5 + [ctypes.c_int] + [I64] * 7 + [VP, ctypes.c_size_t, VP]
+    # token stride below the row size
+    assert fs(*[16] * 6, 1, 32, 8, 64, 128, 0, 65536, 256, 128, 0, 0, 1, 8, None, 0, None) == 1
+    assert _err(lib).startswith("strides:")
+    # strides not multiples of 16
+    assert fs(*[16] * 6, 1, 32, 8, 64, 128, 0, 65536, 264, 2048, 0, 0, 1, 8, None, 0, None) == 1
+    assert _err(lib).startswith("strides:")
+    fp = lib.fqkv_decode_attn_gqa_paged
+    fp.argtypes = [VP] * 8 + [I64] * 8 + [ctypes.c_int] + [I64] * 7 + [VP, ctypes.c_size_t, VP]
+    ok = [16] * 8
+    assert fp(*ok, 1, 32, 8, 10, 4, 24, 64, 128, 0, 4096, 256, 2048, 0, 0, 1, 8, None, 0, None) == 1
+    assert _err(lib).startswith("page_size:")
+    assert fp(*ok[:5], None, 16, 16, 1, 32, 8, 10, 4, 16, 64, 128, 0, 4096, 256, 2048, 0, 0, 1, 8, None, 0, None) == 1
+    assert "null page table" in _err(lib)
+    assert fp(*ok, 1, 32, 8, 0, 4, 16, 64, 128, 0, 4096, 256, 2048, 0, 0, 1, 8, None, 0, None) == 1
+    assert _err(lib).startswith("pages:")

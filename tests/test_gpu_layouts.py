@@ -1,0 +1,135 @@
+"""KV layouts beyond the reference's contiguous [B, Hkv, N, D]: the token-major
+[B, N, Hkv, D] layout FlashInfer uses (flashinfer_looptimed.py:63-65) and paged
+caches (NHD pages, HND pages as a strided view), for fp16, int8 and int4, with
+ragged sequence lengths. Checked against the float64 oracle at max-abs 2e-3;
+the token-major layout also bit for bit against the contiguous entry point,
+since only addresses differ."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import fqkv_decode as fq
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def draw(g, *shape):
+    return torch.randn(*shape, generator=g, dtype=torch.float32)
+
+
+def maxerr(out, ref):
+    return float(np.abs(out.float().cpu().numpy().astype(np.float64) - ref).max())
+
+
+def quantize(fmt, X):
+    if fmt == "int8":
+        q, s = fq.quantize_int8_per_token(X.cuda())
+        return q, s, oracle.dequant_int8(q.cpu().numpy(), s.cpu().numpy())
+    q, s = fq.quantize_int4_per_token(X.cuda())
+    return q, s, oracle.dequant_int4(q.cpu().numpy(), s.cpu().numpy())
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,D", [(2, 32, 8, 1000, 128), (1, 32, 8, 16384, 64), (3, 8, 8, 17, 128)])
+def test_nhd_fp16_equals_contiguous(B, Hq, Hkv, N, D):
+    g = torch.Generator().manual_seed(50)
+    q, K, V = draw(g, B, Hq, D).half(), draw(g, B, Hkv, N, D).half(), draw(g, B, Hkv, N, D).half()
+    a = fq.decode_attn_gqa(q.cuda(), K.cuda(), V.cuda(), 8)
+    b = fq.decode_attn_gqa_nhd(q.cuda(), K.permute(0, 2, 1, 3).contiguous().cuda(),
+                               V.permute(0, 2, 1, 3).contiguous().cuda(), 8)
+    assert torch.equal(a, b)
+    assert maxerr(b, oracle.gqa_attention(q.numpy(), K.numpy(), V.numpy())) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_nhd_quantized(fmt):
+    g = torch.Generator().manual_seed(51)
+    B, Hq, Hkv, N, D = 2, 16, 4, 777, 128
+    q = draw(g, B, Hq, D).half()
+    Kq, Ks, Kf = quantize(fmt, draw(g, B, N, Hkv, D))
+    Vq, Vs, Vf = quantize(fmt, draw(g, B, N, Hkv, D))
+    out = fq.decode_attn_gqa_nhd(q.cuda(), Kq, Vq, 8, Ks, Vs)
+    ref = oracle.gqa_attention(q.numpy(), Kf.transpose(0, 2, 1, 3), Vf.transpose(0, 2, 1, 3))
+    assert maxerr(out, ref) <= TOL
+
+
+def paged_cache(g, lens, Hkv, D, page, fmt, hnd=False, spare=3):
+    """Scatter per-sequence K/V into pages at shuffled page ids; returns the
+    device pages (NHD views), page table, lengths and the float64 per-sequence caches."""
+    npages = [(L + page - 1) // page for L in lens]
+    P = sum(npages) + spare
+    ids = torch.randperm(P, generator=g)
+    max_pages = max(npages)
+    table = torch.full((len(lens), max_pages), -1, dtype=torch.int32)
+    k = 0
+    for b, n in enumerate(npages):
+        table[b, :n] = ids[k:k + n].to(torch.int32)
+        k += n
+    X = draw(g, 2, P, page, Hkv, D)  # raw K and V pages, NHD
+    if fmt == "fp16":
+        Kp, Vp = X[0].half(), X[1].half()
+        Kf, Vf = Kp.float().numpy(), Vp.float().numpy()
+        Ks = Vs = None
+    else:
+        Kp, Ks, Kf = quantize(fmt, X[0])
+        Vp, Vs, Vf = quantize(fmt, X[1])
+        Kp, Vp, Ks, Vs = Kp.cpu(), Vp.cpu(), Ks.cpu(), Vs.cpu()
+    seqs = []
+    for b, L in enumerate(lens):
+        t = np.arange(L)
+        pid = table[b, t // page].numpy()
+        pos = t % page
+        seqs.append((Kf[pid, pos].transpose(1, 0, 2), Vf[pid, pos].transpose(1, 0, 2)))  # [Hkv, L, D]
+    if hnd:  # store pages head-major, hand the kernel the NHD view
+        Kp = Kp.permute(0, 2, 1, 3).contiguous().cuda().permute(0, 2, 1, 3)
+        Vp = Vp.permute(0, 2, 1, 3).contiguous().cuda().permute(0, 2, 1, 3)
+        if Ks is not None:
+            Ks = Ks.permute(0, 2, 1).contiguous().cuda().permute(0, 2, 1)
+            Vs = Vs.permute(0, 2, 1).contiguous().cuda().permute(0, 2, 1)
+    else:
+        Kp, Vp = Kp.cuda(), Vp.cuda()
+        if Ks is not None:
+            Ks, Vs = Ks.cuda(), Vs.cuda()
+    return Kp, Vp, Ks, Vs, table.cuda(), torch.tensor(lens, dtype=torch.int32).cuda(), seqs
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "int8", "int4"])
+@pytest.mark.parametrize("page,hnd", [(16, False), (64, True), (256, False)])
+def test_paged(fmt, page, hnd):
+    g = torch.Generator().manual_seed(52)
+    lens = [1, 15, 16, 17, 300, 3000]
+    Hq, Hkv, D = 32, 8, 128
+    Kp, Vp, Ks, Vs, table, sl, seqs = paged_cache(g, lens, Hkv, D, page, fmt, hnd)
+    q = draw(g, len(lens), Hq, D).half()
+    out = fq.decode_attn_gqa_paged(q.cuda(), Kp, Vp, table, sl, max(lens), 8, Ks, Vs)
+    for b, (Kb, Vb) in enumerate(seqs):
+        ref = oracle.gqa_attention(q.numpy()[b:b + 1], Kb[None], Vb[None])[0]
+        assert maxerr(out[b], ref) <= TOL, (b, lens[b])
+
+
+def test_paged_d64_long_and_split():
+    """One long sequence (internal split over many pages) and D = 64."""
+    g = torch.Generator().manual_seed(53)
+    lens = [20000]
+    Kp, Vp, Ks, Vs, table, sl, seqs = paged_cache(g, lens, 8, 64, 32, "fp16")
+    q = draw(g, 1, 32, 64).half()
+    out = fq.decode_attn_gqa_paged(q.cuda(), Kp, Vp, table, sl, 20000, 4)
+    ref = oracle.gqa_attention(q.numpy(), seqs[0][0][None], seqs[0][1][None])
+    assert maxerr(out, ref) <= TOL
+
+
+def test_layout_entry_points_reject_bad_input():
+    q = torch.zeros(1, 8, 128, dtype=torch.float16, device="cuda")
+    Kp = torch.zeros(4, 24, 2, 128, dtype=torch.float16, device="cuda")
+    table = torch.zeros(1, 4, dtype=torch.int32, device="cuda")
+    sl = torch.ones(1, dtype=torch.int32, device="cuda")
+    with pytest.raises(RuntimeError, match="page_size"):
+        fq.decode_attn_gqa_paged(q, Kp, Kp, table, sl, 16, 8)
+    with pytest.raises(RuntimeError, match="^shape"):
+        fq.decode_attn_gqa_paged(q, Kp[:, :16], Kp[:, :16], table.long(), sl, 16, 8)
+    Ki = torch.zeros(1, 16, 2, 128, dtype=torch.int8, device="cuda")
+    with pytest.raises(RuntimeError, match="^int8"):
+        fq.decode_attn_gqa_nhd(q, Ki, Ki, 8)
