@@ -292,13 +292,14 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // wave index as a scalar, so tile loops branch per wave, not per lane
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
-  int wg = blockIdx.x;
-  const int s = wg % p.S;
-  wg /= p.S;
-  const int hg = wg % p.ngroups;
-  const int r = wg / p.ngroups;
+  // blockIdx.x = (r * ngroups + hg) * S + s, decomposed with multiply-shift divisions
+  const uint32_t wsg = fast_div(blockIdx.x, p.div_S);
+  const int s = (int)(blockIdx.x - wsg * (uint32_t)p.S);
+  const uint32_t rr = fast_div(wsg, p.div_groups);
+  const int hg = (int)(wsg - rr * (uint32_t)p.ngroups);
+  const int r = (int)rr;
   // KV row r = (sequence b, KV head h); its tokens sit kv_ts bytes apart
-  const int b = r / p.hkv;
+  const int b = (int)fast_div((uint32_t)r, p.div_hkv);
   const int h = r - b * p.hkv;
   const uint32_t ts = (uint32_t)p.kv_ts;
   int nr = p.N;  // tokens of this row
@@ -441,13 +442,15 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     const float mu = (mn == -INFINITY) ? 0.0f : mn;
     const float alpha = fast_exp2((m_run - mu) * p.c);
     // The PV operand carries each fp32 weight w = p * (V scale) as an fp16
-    // pair hi + lo (hi = fp16(w'), lo = fp16(w' - hi)) of w' = w * 2^shift:
-    // two matrix-core steps reproduce the weight to ~2^-22 relative, V being
-    // exact in fp16. The power-of-two shift puts the pass's largest possible
-    // weight just under 2^14, so lo stays clear of the fp16 subnormals (small
-    // per-token scales would otherwise push it there); acc is kept in units
-    // of 2^shift and rescaled exactly when the shift changes.
-    int shift = 13;  // fp16 KV: w = p <= 1
+    // pair hi + lo (hi = fp16(w'), lo = fp16(w' - hi)): two matrix-core steps
+    // reproduce the weight to ~2^-22 relative, V being exact in fp16. For
+    // int8 / int4, w' = w * 2^shift with a power-of-two shift that puts the
+    // pass's largest possible weight just under 2^14, so lo stays clear of the
+    // fp16 subnormals (small per-token scales would otherwise push it there,
+    // against V values up to 127); acc is then kept in units of 2^shift and
+    // rescaled exactly when the shift changes. fp16 weights (w = p <= 1, V
+    // values of unit size) need no shift.
+    int shift = 0;
     if constexpr (F::QUANT) {
       float vmax = 0.0f;
 #pragma unroll
@@ -467,14 +470,14 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       for (int k = 0; k < 4; ++k) {
         const float pw = fast_exp2((x[u][k] - mu) * p.c);
         psum += pw;
-        const float wv = __builtin_amdgcn_ldexpf(pw * (float)vs[u][k], shift);
+        const float wv = F::QUANT ? __builtin_amdgcn_ldexpf(pw * (float)vs[u][k], shift) : pw;
         const _Float16 h = (_Float16)wv;
         phi[u][k] = h;
         plo[u][k] = (_Float16)(wv - (float)h);
       }
     l_run = l_run * alpha + psum;
     m_run = mn;
-    const float acc_alpha = __builtin_amdgcn_ldexpf(alpha, shift - acc_shift);
+    const float acc_alpha = F::QUANT ? __builtin_amdgcn_ldexpf(alpha, shift - acc_shift) : alpha;
     acc_shift = shift;
 #pragma unroll
     for (int c = 0; c < VE; ++c) acc[c] *= acc_alpha;
@@ -495,10 +498,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 
   // ---- wave totals: l over the four lane rows; O^T rows are disjoint ----
   l_run = rows4_sum(l_run);
+  if constexpr (F::QUANT) {
 #pragma unroll
-  for (int c = 0; c < VE; ++c)
+    for (int c = 0; c < VE; ++c)
 #pragma unroll
-    for (int k = 0; k < 4; ++k) acc[c][k] = __builtin_amdgcn_ldexpf(acc[c][k], -acc_shift);
+      for (int k = 0; k < 4; ++k) acc[c][k] = __builtin_amdgcn_ldexpf(acc[c][k], -acc_shift);
+  }
   if (n < HG && n < hcnt) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -615,9 +620,14 @@ static hipError_t launch_partial_d(int hg, const PartialParams& p, int nblocks, 
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& p, int nblocks, int nw,
+hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, int nblocks, int nw,
                           hipStream_t st) {
-  if (nw < 1 || nw > NW_MAX || nblocks < 1) return hipErrorInvalidValue;
+  if (nw < 1 || nw > NW_MAX || nblocks < 1 || params.S < 1 || params.ngroups < 1 || params.hkv < 1)
+    return hipErrorInvalidValue;
+  PartialParams p = params;
+  p.div_S = make_fastdiv((uint32_t)p.S);
+  p.div_groups = make_fastdiv((uint32_t)p.ngroups);
+  p.div_hkv = make_fastdiv((uint32_t)p.hkv);
   switch (fmt) {
     case KV_F16: return D == 64 ? launch_partial_d<KV_F16, 64>(hg, p, nblocks, nw, st)
                                 : launch_partial_d<KV_F16, 128>(hg, p, nblocks, nw, st);

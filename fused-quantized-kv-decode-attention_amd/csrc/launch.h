@@ -8,6 +8,24 @@ namespace fqkv {
 
 constexpr int NW_MAX = 8;  // waves per workgroup the kernels are sized for
 
+// Division by a run-time constant d (1 <= d < 2^31) for numerators below 2^31:
+// n / d = (umulhi(n, magic) + n) >> shift with magic = 2^32 (2^shift - d) / d + 1
+// and shift = ceil(log2 d) (the round-up method of Granlund and Montgomery);
+// umulhi(n, magic) < n, so the sum stays below 2^32.
+struct FastDiv {
+  uint32_t magic;
+  uint32_t shift;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+  uint32_t l = 0;
+  while ((uint64_t(1) << l) < d) ++l;
+  const uint64_t m = ((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1;
+  return FastDiv{(uint32_t)m, l};
+}
+__device__ __forceinline__ uint32_t fast_div(uint32_t n, FastDiv f) {
+  return (__umulhi(n, f.magic) + n) >> f.shift;
+}
+
 // Work item of the partial kernel: blockIdx.x = (r * ngroups + g) * S + s
 // with r the KV row (batch * kv_head), g the query-head group (HG heads of
 // the G query heads that share KV row r) and s the split.
@@ -45,6 +63,8 @@ struct PartialParams {
   int max_pages;
   int page_log2;
   int num_pages;
+  // set by launch_partial from S, ngroups and hkv
+  FastDiv div_S, div_groups, div_hkv;
 };
 
 // The reference's contiguous layout: K, V [rows, N, row_bytes], scales [rows, N].
