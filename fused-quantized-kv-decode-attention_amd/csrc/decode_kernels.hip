@@ -103,112 +103,150 @@ typedef float fl4_t __attribute__((ext_vector_type(4)));
 // that merges a group resets its counter, so every call leaves them at zero.
 __device__ int g_split_arrivals[SPLIT_SLOTS][MAX_SPLIT_GROUPS];
 
-// Merge S split partials for query heads h0 .. h0+nh-1 with the whole
-// workgroup: o[h] = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s
+// Full-wave reductions: DPP within each 16-lane row (quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror), then across the rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, dpp_f<0xB1>(x));
+  x = fmaxf(x, dpp_f<0x4E>(x));
+  x = fmaxf(x, dpp_f<0x141>(x));
+  x = fmaxf(x, dpp_f<0x140>(x));
+  return rows4_max(x);
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  x += dpp_f<0xB1>(x);
+  x += dpp_f<0x4E>(x);
+  x += dpp_f<0x141>(x);
+  x += dpp_f<0x140>(x);
+  return rows4_sum(x);
+}
+
+// Merge S split partials for query heads h0 .. h0+nh-1:
+// o[h] = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s
 // (decode_attn_gqa_sk_fast.cu:57-94; m in natural-log units, an empty split
-// has m = -inf and weight 0). Thread t owns float4 column c of head hh for
-// splits g, g + NG, ...; it issues a chunk of CH splits' loads before the
-// block-wide maximum is known, so a merge costs about one memory round trip.
-// s_acc holds blockDim.x float4, s_red 2 * blockDim.x / (D/4) floats.
-// COHERENT: read the partials with device-scope (sc1) loads, for partials
-// that other workgroups of the same launch stored with device-scope stores.
-template <int D, bool COHERENT>
-__device__ void merge_splits(const float* __restrict__ m_part, const float* __restrict__ l_part,
-                             const float* __restrict__ o_part, _Float16* __restrict__ o, size_t h0,
-                             int nh, int S, fl4_t* s_acc, float* s_red) {
-  constexpr int C4 = D / 4;
-  constexpr int CH = 8;
-  auto ld1 = [](const float* ptr) -> float {
-    if constexpr (COHERENT) return __hip_atomic_load(ptr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    else return *ptr;
+// has m = -inf, l = 0, acc = 0 and weight 0).
+//
+// A unit is one head's 64-dim block; one wave merges one unit: lane s owns the
+// weight of split s of each 64-split block (kept in the wave's own LDS row, so
+// no barrier is needed to share it) and lane d accumulates output dim d over
+// the splits, with up to 64 partial loads in flight. Buffer descriptors bound
+// every load (reads past the last split return zero), so no lane computes a
+// bounds test per load. The m and l loads go out before the first partial
+// chunk, so a merge costs about one memory round trip (two when S > 64).
+// When there are fewer units than waves, the splits of a unit are cut into
+// nsl slices on different waves and the slices meet in LDS (the only
+// barrier; its condition is the same for the whole workgroup).
+// CPOL: cache policy of the partial loads (CPOL_SC1 for partials that other
+// workgroups of the same launch stored at device scope).
+// s_w: 64 floats per wave (16-byte aligned rows); s_red: 65 floats per wave.
+template <int D, int CPOL>
+__device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, const float* __restrict__ l_part,
+                                             const float* __restrict__ o_part, _Float16* __restrict__ o,
+                                             size_t h0, int nh, int S, float (*s_w)[64], float (*s_red)[65]) {
+  constexpr int DB = D / 64;  // units per head
+  constexpr int CHK = 32;     // partial loads per lane per chunk
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nw = blockDim.x >> 6;
+  const int units = nh * DB;
+  // nsl = 2^lg slices per unit; waves wv with equal wv >> lg share a unit
+  int lg = 0;
+  while ((2 << lg) * units <= nw && (2 << lg) * CHK <= S) ++lg;
+  const int nsl = 1 << lg;
+  const int cu = nw >> lg;                                              // units per round
+  const int len = (((S + nsl - 1) >> lg) + CHK - 1) & ~(CHK - 1);      // splits per slice
+  auto ld = [](rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, CPOL));
   };
-  // one descriptor (uniform) over the acc partials of heads h0 .. h0+nh-1
-  const rsrc_t rO = make_rsrc(o_part + h0 * S * D, (uint32_t)(nh * S * D) * 4u);
-  auto ld4 = [&](const fl4_t* base, uint32_t idx) -> fl4_t {
-    if constexpr (COHERENT) {
-      const uint32_t off = (uint32_t)((const float*)(base + idx) - (o_part + h0 * S * D)) * 4u;
-      return __builtin_bit_cast(fl4_t, __builtin_amdgcn_raw_buffer_load_b128(rO, (int)off, 0, CPOL_SC1));
-    } else {
-      return base[idx];
-    }
+  // partial loads: lane offset in a VGPR, the split's row offset as a scalar
+  auto ldo = [](rsrc_t r, uint32_t lane_off, uint32_t row_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)lane_off, (int)row_off, CPOL));
   };
-  const int t = threadIdx.x;
-  const int nt = blockDim.x;
-  const int hpr = nt / C4;  // heads per round (>= 4: nt >= 128, C4 <= 32)
-  float* s_mx = s_red;
-  float* s_l = s_red + hpr;
-  for (int hb = 0; hb < nh; hb += hpr) {
-    const int hr = min(hpr, nh - hb);
-    const int NG = nt / (C4 * hr);
-    const int c = t % C4;
-    const int hh = (t / C4) % hr;
-    const int g = t / (C4 * hr);
-    const bool act = g < NG;
-    const size_t h = h0 + hb + hh;
-    const float* mh = m_part + h * S;
-    const float* lh = l_part + h * S;
-    const fl4_t* oh = reinterpret_cast<const fl4_t*>(o_part + h * S * D);
-    fl4_t ov[CH];
-    float mv[CH], lv[CH];
+  for (int ub = 0; ub < units; ub += cu) {  // a single round when nsl > 1
+    const int u = ub + (wv >> lg);
+    const int sl = wv & (nsl - 1);
+    const int h = u / DB;
+    const int db = u - h * DB;
+    const int start = sl * len;
+    const int end = min(S, start + len);
+    const bool live = (wv >> lg) < cu && u < units && start < end;  // wave-uniform
+    float acc = 0.0f, L = 0.0f;
+    if (live) {
+      const size_t hrow = h0 + h;
+      const rsrc_t rM = make_rsrc(m_part + hrow * S, (uint32_t)S * 4u);
+      const rsrc_t rL = make_rsrc(l_part + hrow * S, (uint32_t)S * 4u);
+      // split start + k, dim lane at byte (k D + lane) 4; the record ends with
+      // the last split's 64 dims
+      const rsrc_t rO = make_rsrc(o_part + (hrow * S + start) * D + db * 64,
+                                  (uint32_t)(end - start - 1) * D * 4u + 256u);
+      const uint32_t lo4 = (uint32_t)lane * 4u;
+      const float m0 = ld(rM, lo4);
+      const float l0 = ld(rL, lo4);
+      float ov[CHK];
 #pragma unroll
-    for (int k = 0; k < CH; ++k) {
-      const int sk = g + k * NG;
-      const bool ok = act && sk < S;
-      ov[k] = ok ? ld4(oh, (uint32_t)(sk * C4 + c)) : fl4_t{0.0f, 0.0f, 0.0f, 0.0f};
-      mv[k] = ok ? ld1(mh + sk) : -INFINITY;
-      lv[k] = ok ? ld1(lh + sk) : 0.0f;
-    }
-    float mloc = -INFINITY;
+      for (int k = 0; k < CHK; ++k) ov[k] = ldo(rO, lo4, (uint32_t)(k * D * 4));
+      float M = lane < S ? m0 : -INFINITY;
+      for (int s0 = 64; s0 < S; s0 += 64) {
+        const float mm = ld(rM, lo4 + (uint32_t)s0 * 4u);
+        M = fmaxf(M, s0 + lane < S ? mm : -INFINITY);
+      }
+      M = wave_max(M);
+      if (M == -INFINITY) M = 0.0f;  // every split empty: all weights 0
+      auto accumulate = [&](int c0) {
+        const fl4_t* w4 = reinterpret_cast<const fl4_t*>(&s_w[wv][c0 & 63]);
 #pragma unroll
-    for (int k = 0; k < CH; ++k) mloc = fmaxf(mloc, mv[k]);
-    if (act)
-      for (int sk = g + CH * NG; sk < S; sk += NG) mloc = fmaxf(mloc, ld1(mh + sk));
-    if (act && c == 0) s_mx[g * hr + hh] = mloc;
-    __syncthreads();
-    float M = -INFINITY;
-    for (int gg = 0; gg < NG; ++gg) M = fmaxf(M, s_mx[gg * hr + hh]);
-    fl4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    float L = 0.0f;
-    if (act && M != -INFINITY) {
-      for (int base = 0;; base += CH * NG) {
-#pragma unroll
-        for (int k = 0; k < CH; ++k) {
-          const float sc = fast_exp2((mv[k] - M) * LOG2E);
-          L += sc * lv[k];
-          acc += sc * ov[k];
+        for (int k = 0; k < CHK / 4; ++k) {
+          const fl4_t wk = w4[k];
+          acc = fmaf(wk.x, ov[4 * k], acc);
+          acc = fmaf(wk.y, ov[4 * k + 1], acc);
+          acc = fmaf(wk.z, ov[4 * k + 2], acc);
+          acc = fmaf(wk.w, ov[4 * k + 3], acc);
         }
-        const int nb = base + CH * NG;
-        if (nb >= S) break;
+      };
+      for (int c0 = start; c0 < end; c0 += CHK) {
+        const int b = c0 >> 6;
+        if (c0 == start || (c0 & 63) == 0) {  // weights of splits 64 b .. 64 b + 63 in this slice
+          float mm = m0, ll = l0;
+          if (b > 0) {
+            mm = ld(rM, lo4 + (uint32_t)b * 256u);
+            ll = ld(rL, lo4 + (uint32_t)b * 256u);
+          }
+          const int sk = 64 * b + lane;
+          const float w = sk >= start && sk < end ? fast_exp2((mm - M) * LOG2E) : 0.0f;
+          L = fmaf(w, ll, L);
+          s_w[wv][lane] = w;
+        }
+        const int c1 = c0 + CHK;
+        if (c1 < end) {
+          float nv[CHK];
 #pragma unroll
-        for (int k = 0; k < CH; ++k) {
-          const int sk = nb + g + k * NG;
-          const bool ok = sk < S;
-          ov[k] = ok ? ld4(oh, (uint32_t)(sk * C4 + c)) : fl4_t{0.0f, 0.0f, 0.0f, 0.0f};
-          mv[k] = ok ? ld1(mh + sk) : -INFINITY;
-          lv[k] = ok ? ld1(lh + sk) : 0.0f;
+          for (int k = 0; k < CHK; ++k) nv[k] = ldo(rO, lo4, (uint32_t)((c1 - start + k) * D * 4));
+          accumulate(c0);
+#pragma unroll
+          for (int k = 0; k < CHK; ++k) ov[k] = nv[k];
+        } else {
+          accumulate(c0);
         }
       }
+      L = wave_sum(L);
     }
-    s_acc[t] = acc;
-    if (act && c == 0) s_l[g * hr + hh] = L;
-    __syncthreads();
-    if (t < hr * C4) {
-      const int oh2 = t / C4;
-      const int c2 = t % C4;
-      fl4_t r = {0.0f, 0.0f, 0.0f, 0.0f};
-      float Lt = 0.0f;
-      for (int gg = 0; gg < NG; ++gg) {
-        r += s_acc[(gg * hr + oh2) * C4 + c2];
-        Lt += s_l[gg * hr + oh2];
+    if (nsl > 1) {
+      if (live) {
+        s_red[wv][lane] = acc;
+        if (lane == 0) s_red[wv][64] = L;
       }
-      r /= Lt;
-      _Float16* dst = o + (h0 + hb + oh2) * D + 4 * c2;
-      dst[0] = (_Float16)r.x;
-      dst[1] = (_Float16)r.y;
-      dst[2] = (_Float16)r.z;
-      dst[3] = (_Float16)r.w;
+      __syncthreads();
+      if (live && sl == 0)
+        for (int q = 1; q < nsl; ++q) {
+          if ((q * len) >= S) break;  // empty slice
+          acc += s_red[wv + q][lane];
+          L += s_red[wv + q][64];
+        }
     }
-    __syncthreads();
+    if (live && sl == 0) o[(h0 + h) * D + db * 64 + lane] = (_Float16)(acc / L);
   }
 }
 
@@ -284,8 +322,8 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   __shared__ float s_o[NW_MAX][HG][opitch<D>()];
   __shared__ float s_m[HG][NW_MAX];
   __shared__ float s_l[HG][NW_MAX];
-  __shared__ fl4_t s_macc[64 * NW_MAX];  // in-kernel split merge
-  __shared__ float s_mred[2 * 64 * NW_MAX / (D / 4)];
+  __shared__ __attribute__((aligned(16))) float s_mw[NW_MAX][64];  // in-kernel split merge
+  __shared__ float s_mr[NW_MAX][65];
   __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
@@ -539,14 +577,16 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-      int* ctr = &g_split_arrivals[p.slot][blockIdx.x / p.S];
-      const int prev = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int last = prev == p.S - 1;
-      if (last) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      s_last = last;
+      int* ctr = &g_split_arrivals[p.slot][wsg];
+      s_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.S - 1;
     }
     __syncthreads();
-    if (s_last) merge_splits<D, true>(p.m_part, p.l_part, p.o_part, p.o, qrow0, hcnt, p.S, s_macc, s_mred);
+    if (s_last) {
+      merge_splits<D, CPOL_SC1>(p.m_part, p.l_part, p.o_part, p.o, qrow0, hcnt, p.S, s_mw, s_mr);
+      // every workgroup of the group has counted in: reset for the next call
+      if (threadIdx.x == 0)
+        __hip_atomic_store(&g_split_arrivals[p.slot][wsg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -557,9 +597,9 @@ __global__ void __launch_bounds__(64 * NW_MAX) combine_kernel(const float* __res
                                                               const float* __restrict__ l_part,
                                                               const float* __restrict__ o_part,
                                                               _Float16* __restrict__ o, int S) {
-  __shared__ fl4_t s_acc[64 * NW_MAX];
-  __shared__ float s_red[2 * 64 * NW_MAX / (D / 4)];
-  merge_splits<D, false>(m_part, l_part, o_part, o, blockIdx.x, 1, S, s_acc, s_red);
+  __shared__ __attribute__((aligned(16))) float s_w[NW_MAX][64];
+  __shared__ float s_red[NW_MAX][65];
+  merge_splits<D, 0>(m_part, l_part, o_part, o, blockIdx.x, 1, S, s_w, s_red);
 }
 
 // Dequantise through the kernels' own conversions (K side: int -> fp16
