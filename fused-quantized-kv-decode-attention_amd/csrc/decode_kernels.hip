@@ -315,8 +315,7 @@ template <int FMT, int D, int HG, bool PAGED>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
   using VG = VGeom<F::ROWB, D>;
-  // tiles per pass (int8 at D = 128 converts more K per tile: three fit the registers)
-  constexpr int U = (FMT == KV_I8 && D == 128) ? 3 : 4;
+  constexpr int U = TILES_PER_PASS;
   constexpr int VE = VG::VE;   // PV steps per tile
   constexpr int VD = VG::VD;   // dwords per V chunk
   __shared__ float s_o[NW_MAX][HG][opitch<D>()];
@@ -662,8 +661,16 @@ static hipError_t launch_partial_d(int hg, const PartialParams& p, int nblocks, 
 
 hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, int nblocks, int nw,
                           hipStream_t st) {
-  if (nw < 1 || nw > NW_MAX || nblocks < 1 || params.S < 1 || params.ngroups < 1 || params.hkv < 1)
+  if ((nw != 2 && nw != 4 && nw != 8) || nblocks < 1 || params.S < 1 || params.ngroups < 1 || params.hkv < 1)
     return hipErrorInvalidValue;
+  // nw is a maximum: a split shorter than one pass of nw waves would leave
+  // waves with nothing to load, so take the fewest waves (at least 2) that
+  // still cover the split in one pass -- but, when the splits are merged in
+  // the kernel, no fewer than the merge has (head, 64-dim block) units, so
+  // that every unit keeps a wave of its own.
+  const int tiles = (params.chunk + 15) / 16;
+  const int units = params.S > 1 ? hg * (D / 64) : 1;
+  while (nw > 2 && nw / 2 >= units && (nw / 2) * TILES_PER_PASS >= tiles) nw /= 2;
   PartialParams p = params;
   p.div_S = make_fastdiv((uint32_t)p.S);
   p.div_groups = make_fastdiv((uint32_t)p.ngroups);

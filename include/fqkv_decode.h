@@ -21,6 +21,11 @@
  * Alignment: q, K, V and o_part 16 bytes (K, V 8 bytes for int4 at D = 64);
  * o, scales 2 bytes. Each K or V row block (N rows) must span < 4 GiB.
  *
+ * W (and CW) count 64-lane waves per workgroup. W is a maximum: a split too
+ * short to give every wave a full pass of 4 16-token tiles runs on fewer
+ * waves (at least 2). Results do not depend on W, CW or S beyond fp32
+ * rounding of the merge order.
+ *
  * Return value: FQKV_OK (0) on success; otherwise a non-zero FQKV_ERR_* code
  * and fqkv_last_error() describes the failure (thread-local). Argument
  * checks run before any HIP call.
