@@ -29,8 +29,10 @@
 // Waves of a workgroup take interleaved tiles; their (m, l, acc) states are
 // merged through LDS. With one split the workgroup writes the normalised
 // fp16 output; otherwise it writes the reference's fp32 scratch layout
-// (m_part[h*S+s], l_part[h*S+s], o_part[(h*S+s)*D+d]) and the combine
-// kernel merges the splits.
+// (m_part[h*S+s], l_part[h*S+s], o_part[(h*S+s)*D+d]), and the last of the
+// S workgroups of its (KV row, head group) to finish merges the splits in
+// the same launch (or, without an arrival-counter slot, the combine kernel
+// does in a second launch).
 //
 // Reference algorithm: decode_attn_gqa_sk_fast.cu:6-54 (partial),
 // :57-94 (combine); decode_attn_fp16_mw.cu:6-49 and decode_attn_gqa.cu:8-55

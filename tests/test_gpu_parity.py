@@ -234,6 +234,21 @@ def test_gqa_sk_fast_knob_invariance(merge_mode):
                 assert maxerr(run_sk(q, K, V, S, W, CW)[0], ref) <= TOL, (S, W, CW)
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("S,W", [(100, 8), (256, 8), (700, 8), (257, 2)])
+def test_gqa_sk_fast_one_head_per_kv_row(D, S, W, merge_mode):
+    """Hq = Hkv with many splits: the merge cuts each head's splits into slices
+    on several waves (and S > 256 takes the extra m blocks)."""
+    Hq, Hkv, N = 2, 2, 6000
+    g = torch.Generator().manual_seed(14)
+    q, K, V = draw(g, Hq, D).half(), draw(g, Hkv, N, D).half(), draw(g, Hkv, N, D).half()
+    ref = oracle.gqa_attention(q.numpy()[None], K.numpy()[None], V.numpy()[None])[0]
+    o, mp, lp, op = run_sk(q, K, V, S, W, 8)
+    assert maxerr(o, ref) <= TOL
+    m, l, acc = oracle.split_partials(q.numpy(), K.numpy(), V.numpy(), S)
+    assert maxerr(o, oracle.combine_partials(m, l, acc)) <= TOL
+
+
 def test_gqa_sk_fast_batch_folds_into_heads(merge_mode):
     """Batch B as q [B*Hq, D], K [B*Hkv, N, D]: head b*Hq+j reads KV row b*Hkv + j/G."""
     B, Hq, Hkv, N, D = 3, 32, 8, 2048, 128
