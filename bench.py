@@ -515,14 +515,23 @@ def suite_llama(torch, fq, rows):
     torch.cuda.empty_cache()
 
 
-def run_suite(torch, fq, path, steps=400, warmup=40):
+SUITES = ("mha_small", "mha_quant", "gqa", "splitk", "splitk_quant", "llama")
+
+
+def run_suite(torch, fq, path, steps=400, warmup=40, only=SUITES):
     rows = []
-    suite_mha_small(torch, fq, steps, warmup, rows)
-    suite_mha_quant(torch, fq, steps, warmup, rows)
-    suite_gqa(torch, fq, steps, warmup, rows)
-    suite_splitk(torch, fq, steps, warmup, rows)
-    suite_splitk_quant(torch, fq, steps, warmup, rows)
-    suite_llama(torch, fq, rows)
+    if "mha_small" in only:
+        suite_mha_small(torch, fq, steps, warmup, rows)
+    if "mha_quant" in only:
+        suite_mha_quant(torch, fq, steps, warmup, rows)
+    if "gqa" in only:
+        suite_gqa(torch, fq, steps, warmup, rows)
+    if "splitk" in only:
+        suite_splitk(torch, fq, steps, warmup, rows)
+    if "splitk_quant" in only:
+        suite_splitk_quant(torch, fq, steps, warmup, rows)
+    if "llama" in only:
+        suite_llama(torch, fq, rows)
     with open(path, "w") as f:
         for r in rows:
             f.write(json.dumps(r) + "\n")
@@ -544,9 +553,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--suite", metavar="FILE", default="",
                     help="also measure the secondary configurations, JSON lines into FILE")
+    ap.add_argument("--suite-only", metavar="NAMES", default=",".join(SUITES),
+                    help="comma-separated subset of the suite: " + ", ".join(SUITES))
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
+    only = tuple(x for x in args.suite_only.split(",") if x)
+    unknown = [x for x in only if x not in SUITES]
+    if unknown:
+        print("unknown suite name(s): %s (choose from %s)" % (", ".join(unknown), ", ".join(SUITES)), file=sys.stderr)
+        sys.exit(2)
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -647,7 +663,7 @@ def main():
     if args.suite:
         del Ks, Vs
         torch.cuda.empty_cache()
-        run_suite(torch, fq, args.suite)
+        run_suite(torch, fq, args.suite, only=only)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)
