@@ -197,15 +197,17 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
       }
       M = wave_max(M);
       if (M == -INFINITY) M = 0.0f;  // every split empty: all weights 0
+      // four independent sums, so the FMAs do not wait on each other
+      fl4_t acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
       auto accumulate = [&](int c0) {
         const fl4_t* w4 = reinterpret_cast<const fl4_t*>(&s_w[wv][c0 & 63]);
 #pragma unroll
         for (int k = 0; k < CHK / 4; ++k) {
           const fl4_t wk = w4[k];
-          acc = fmaf(wk.x, ov[4 * k], acc);
-          acc = fmaf(wk.y, ov[4 * k + 1], acc);
-          acc = fmaf(wk.z, ov[4 * k + 2], acc);
-          acc = fmaf(wk.w, ov[4 * k + 3], acc);
+          acc4.x = fmaf(wk.x, ov[4 * k], acc4.x);
+          acc4.y = fmaf(wk.y, ov[4 * k + 1], acc4.y);
+          acc4.z = fmaf(wk.z, ov[4 * k + 2], acc4.z);
+          acc4.w = fmaf(wk.w, ov[4 * k + 3], acc4.w);
         }
       };
       for (int c0 = start; c0 < end; c0 += CHK) {
@@ -233,6 +235,7 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
           accumulate(c0);
         }
       }
+      acc = (acc4.x + acc4.y) + (acc4.z + acc4.w);
       L = wave_sum(L);
     }
     if (nsl > 1) {
