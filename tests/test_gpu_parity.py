@@ -261,6 +261,18 @@ def test_gqa_sk_fast_batch_folds_into_heads(merge_mode):
     assert float((o.float() - o2.float()).abs().max()) <= TOL
 
 
+def test_split_merge_more_groups_than_counters():
+    """More (KV row, head group) pairs than one counter slot holds (16384):
+    the call falls back to the partial + combine launch pair, same result."""
+    Hq = Hkv = 16400
+    N, D, S = 20, 64, 3
+    g = torch.Generator().manual_seed(15)
+    q, K, V = draw(g, Hq, D).half(), draw(g, Hkv, N, D).half(), draw(g, Hkv, N, D).half()
+    o, mp, lp, op = run_sk(q, K, V, S, 2, 4)
+    ref = oracle.gqa_attention(q.numpy()[None], K.numpy()[None], V.numpy()[None])[0]
+    assert maxerr(o, ref) <= TOL
+
+
 def test_split_merge_many_calls_in_a_row():
     """More consecutive split calls than arrival-counter slots, with changing
     shapes: every result stays correct (counters are reset by each merge)."""
