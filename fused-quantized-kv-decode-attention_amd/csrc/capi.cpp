@@ -95,7 +95,7 @@ int64_t splits_for(int64_t rows, int64_t G, int64_t N, int fmt, int64_t W, int c
 }
 
 // Internal split scratch: m [heads*S], l [heads*S], then acc [heads*S*D]
-// starting on a 16-byte boundary (the combine kernel reads it as float4).
+// starting on a 16-byte boundary, so every partial row is 16-byte aligned.
 size_t acc_offset_floats(int64_t heads, int64_t S) { return (size_t)((2 * heads * S + 3) & ~(int64_t)3); }
 size_t scratch_bytes(int64_t heads, int64_t S, int64_t D) {
   return (acc_offset_floats(heads, S) + (size_t)heads * (size_t)S * (size_t)D) * sizeof(float);

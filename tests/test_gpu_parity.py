@@ -348,6 +348,35 @@ def test_runs_on_current_stream_and_in_graphs():
         assert torch.equal(o, eager)
 
 
+def test_split_calls_on_concurrent_streams():
+    """Split calls in flight on four streams at once (each call takes its own
+    arrival-counter slot): every output equals the same call run alone."""
+    Hq, Hkv, N, D, S = 32, 8, 3000, 128, 24
+    g = torch.Generator().manual_seed(16)
+    calls = []
+    for i in range(8):
+        q, K, V = gpu(draw(g, Hq, D).half()), gpu(draw(g, Hkv, N, D).half()), gpu(draw(g, Hkv, N, D).half())
+        scratch = (torch.empty(Hq, S, device=DEV), torch.empty(Hq, S, device=DEV), torch.empty(Hq, S, D, device=DEV))
+        o = torch.empty(Hq, D, dtype=torch.float16, device=DEV)
+        calls.append((q, K, V, scratch, o))
+    alone = []
+    for q, K, V, (mp, lp, op), o in calls:
+        fq.gqa_sk_fast(q, K, V, mp, lp, op, o, S, 8, 8)
+        alone.append(o.clone())
+        o.zero_()
+    streams = [torch.cuda.Stream() for _ in range(4)]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+    for i, (q, K, V, (mp, lp, op), o) in enumerate(calls):
+        with torch.cuda.stream(streams[i % 4]):
+            fq.gqa_sk_fast(q, K, V, mp, lp, op, o, S, 8, 8)
+    for st in streams:
+        torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    for (_, _, _, _, o), ref in zip(calls, alone):
+        assert torch.equal(o, ref)
+
+
 def test_binding_error_messages():
     q = torch.zeros(2, 64, dtype=torch.float16, device=DEV)
     K = torch.zeros(2, 16, 64, dtype=torch.float16, device=DEV)
