@@ -463,25 +463,29 @@ def suite_llama(torch, fq, rows):
         for layer in model.model.layers:
             layer.self_attn.config._attn_implementation = impl
 
-    def tok_per_s(impl, prompt_len=512, gen=128, reps=3):
+    def cache(kv_format):
+        return None if kv_format is None else hf_llama.QuantizedKVCache(cfg, kv_format)
+
+    def tok_per_s(impl, prompt_len=512, gen=128, reps=3, kv_format=None):
         set_impl(impl)
         ids = torch.randint(0, cfg.vocab_size, (1, prompt_len), device="cuda")
         best = 1e9
         with torch.no_grad():
-            model.generate(ids, max_new_tokens=8, min_new_tokens=8, do_sample=False)
+            model.generate(ids, max_new_tokens=8, min_new_tokens=8, do_sample=False, past_key_values=cache(kv_format))
             torch.cuda.synchronize()
             for _ in range(reps):
                 t0 = time.perf_counter()
-                model.generate(ids, max_new_tokens=gen, min_new_tokens=gen, do_sample=False)
+                model.generate(ids, max_new_tokens=gen, min_new_tokens=gen, do_sample=False,
+                               past_key_values=cache(kv_format))
                 torch.cuda.synchronize()
                 best = min(best, time.perf_counter() - t0)
         return gen / best
 
-    def decode_ms(impl, ctx, reps=100):
+    def decode_ms(impl, ctx, reps=100, kv_format=None):
         set_impl(impl)
         with torch.no_grad():
             ids = torch.randint(0, cfg.vocab_size, (1, ctx), device="cuda")
-            out = model(ids, use_cache=True)
+            out = model(ids, use_cache=True, past_key_values=cache(kv_format))
             past = out.past_key_values
             step = torch.randint(0, cfg.vocab_size, (1, 1), device="cuda")
             ts = []
@@ -504,12 +508,22 @@ def suite_llama(torch, fq, rows):
     for ctx in (512, 2048, 8192):
         r["decode_ms_sdpa_ctx%d" % ctx] = round(decode_ms("sdpa", ctx), 4)
         r["decode_ms_kernel_ctx%d" % ctx] = round(decode_ms(name, ctx), 4)
+    # the same hook over an int8 / int4 KV cache (hf_llama.QuantizedKVCache); KV bytes read per
+    # decode step at 8192 cached tokens: 16 layers x 2 x 8 heads x 8192 x (128, 64 + 2, 32 + 2) B
+    for fmt in ("int8", "int4"):
+        r["kernel_%s_tok_s" % fmt] = round(tok_per_s(name, kv_format=fmt), 2)
+        r["decode_ms_kernel_%s_ctx8192" % fmt] = round(decode_ms(name, 8192, kv_format=fmt), 4)
+    r["kv_mb_per_step_ctx8192"] = {f: round(16 * 2 * 8 * 8192 * b / 1e6, 1)
+                                   for f, b in (("fp16", 128), ("int8", 66), ("int4", 34))}
     rows.append(r)
     log("llama     generate tok/s: sdpa %.2f, kernel %.2f; decode step ms (sdpa/kernel) ctx512 %.3f/%.3f "
         "ctx2048 %.3f/%.3f ctx8192 %.3f/%.3f" % (r["sdpa_tok_s"], r["kernel_tok_s"], r["decode_ms_sdpa_ctx512"],
                                                  r["decode_ms_kernel_ctx512"], r["decode_ms_sdpa_ctx2048"],
                                                  r["decode_ms_kernel_ctx2048"], r["decode_ms_sdpa_ctx8192"],
                                                  r["decode_ms_kernel_ctx8192"]))
+    log("llama     int8 / int4 KV cache: generate tok/s %.2f / %.2f; decode step ms ctx8192 %.3f / %.3f"
+        % (r["kernel_int8_tok_s"], r["kernel_int4_tok_s"], r["decode_ms_kernel_int8_ctx8192"],
+           r["decode_ms_kernel_int4_ctx8192"]))
     set_impl("sdpa")
     del model
     torch.cuda.empty_cache()

@@ -379,6 +379,44 @@ torch::Tensor decode_attn_gqa_nhd(torch::Tensor q, torch::Tensor K, torch::Tenso
   return o;
 }
 
+// decode_attn_gqa_strided(q[B,Hq,D], K[B,Hkv,N,D or D/2], V, W, Ks=None[B,Hkv,N], Vs=None) -> o[B,Hq,D]:
+// K and V may be any strided views with contiguous rows (the last dim), e.g. the first N tokens of a
+// preallocated [B,Hkv,capacity,D] cache, or a token-major [B,N,Hkv,D] cache passed as transpose(1,2);
+// the scales are views of the same kind. The strides must satisfy fqkv_decode_attn_gqa_strided's rules.
+torch::Tensor decode_attn_gqa_strided(torch::Tensor q, torch::Tensor K, torch::Tensor V, int64_t W,
+                                      c10::optional<torch::Tensor> Ks, c10::optional<torch::Tensor> Vs) {
+  check_gpu({&q});
+  check_gpu_strided({&K, &V}, q);
+  check_half(q, "q");
+  TORCH_CHECK(q.dim() == 3 && K.dim() == 4 && V.sizes() == K.sizes() && V.strides() == K.strides() &&
+                  V.scalar_type() == K.scalar_type() && q.size(0) == K.size(0),
+              "shape: expected q [B,Hq,D], K and V [B,Hkv,N,D] views with equal strides; got q ", q.sizes(),
+              ", K ", K.sizes(), " ", K.strides(), ", V ", V.sizes(), " ", V.strides());
+  TORCH_CHECK(K.size(3) == 1 || K.stride(3) == 1, "contig: K and V rows (the last dim) must be contiguous");
+  int64_t D = 0, elem = 0;
+  const int fmt = kv_format_of(K, &D, &elem);
+  check_D(D);
+  TORCH_CHECK(q.size(2) == D, "shape: q head_dim ", q.size(2), " does not match KV head_dim ", D);
+  const int64_t B = q.size(0), Hq = q.size(1), Hkv = K.size(1), N = K.size(2);
+  check_W(W);
+  TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
+  TORCH_CHECK(N >= 1, "N: need at least one cached token");
+  check_scales(fmt, Ks, Vs, {B, Hkv, N});
+  if (fmt != FQKV_KV_F16) TORCH_CHECK(Ks->device() == q.device(), "cuda: all tensors must be on the same device");
+  const c10::DeviceGuard guard(q.device());
+  auto o = torch::empty({B, Hq, D}, q.options());
+  auto ws = workspace_for(q, B * Hkv, Hq / Hkv, N, D, fmt, W);
+  const bool quant = fmt != FQKV_KV_F16;
+  check_rc(fqkv_decode_attn_gqa_strided(q.data_ptr(), K.data_ptr(), V.data_ptr(), quant ? Ks->data_ptr() : nullptr,
+                                        quant ? Vs->data_ptr() : nullptr, o.data_ptr(), B, Hq, Hkv, N, D, fmt,
+                                        K.stride(0) * elem, K.stride(1) * elem, K.stride(2) * elem,
+                                        quant ? Ks->stride(0) : 0, quant ? Ks->stride(1) : 0,
+                                        quant ? Ks->stride(2) : 1, W, ws.defined() ? ws.data_ptr() : nullptr,
+                                        ws.defined() ? ws.numel() : 0, cur_stream(q)),
+           "launch");
+  return o;
+}
+
 // decode_attn_gqa_paged(q[B,Hq,D], K_pages[P,page_size,Hkv,D or D/2], V_pages, page_table[B,max_pages] int32,
 //                       seq_lens[B] int32, max_seq_len, W, Ks_pages=None[P,page_size,Hkv], Vs_pages=None)
 // -> o[B,Hq,D]. The page tensors may be any strided view whose last dim is contiguous, so HND
@@ -520,6 +558,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("decode_attn_gqa_nhd", &decode_attn_gqa_nhd, "GQA decode over a token-major [B,N,Hkv,D] KV cache",
         py::arg("q"), py::arg("K"), py::arg("V"), py::arg("W"), py::arg("Ks") = py::none(),
         py::arg("Vs") = py::none());
+  m.def("decode_attn_gqa_strided", &decode_attn_gqa_strided,
+        "GQA decode over [B,Hkv,N,D] KV views with any strides (contiguous rows)", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("W"), py::arg("Ks") = py::none(), py::arg("Vs") = py::none());
   m.def("decode_attn_gqa_paged", &decode_attn_gqa_paged, "GQA decode over a paged KV cache", py::arg("q"),
         py::arg("K_pages"), py::arg("V_pages"), py::arg("page_table"), py::arg("seq_lens"), py::arg("max_seq_len"),
         py::arg("W"), py::arg("Ks_pages") = py::none(), py::arg("Vs_pages") = py::none());

@@ -20,6 +20,9 @@ Beyond the reference (same conventions, no counterpart there):
                                                     the KV quantizers as GPU kernels
     decode_attn_gqa_nhd(q[B,Hq,D], K[B,N,Hkv,D], V, W, Ks=None, Vs=None) -> o[B,Hq,D]
                                                     token-major (FlashInfer NHD) KV layout
+    decode_attn_gqa_strided(q[B,Hq,D], K[B,Hkv,N,D] view, V, W, Ks=None, Vs=None) -> o[B,Hq,D]
+                                                    any strided KV view with contiguous rows
+                                                    (e.g. the filled part of a preallocated cache)
     decode_attn_gqa_paged(q, K_pages[P,page,Hkv,D], V_pages, page_table[B,max_pages], seq_lens[B],
         max_seq_len, W, Ks_pages=None, Vs_pages=None) -> o[B,Hq,D]      paged KV cache
 
@@ -53,6 +56,7 @@ __all__ = [
     "quantize_int8_per_token",
     "quantize_int4_per_token",
     "decode_attn_gqa_nhd",
+    "decode_attn_gqa_strided",
     "decode_attn_gqa_paged",
     "load",
     "lib_path",
@@ -62,7 +66,7 @@ __all__ = [
 _ENTRY_POINTS = ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa",
                  "gqa_sk_fast", "decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8",
                  "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token",
-                 "decode_attn_gqa_nhd", "decode_attn_gqa_paged")
+                 "decode_attn_gqa_nhd", "decode_attn_gqa_strided", "decode_attn_gqa_paged")
 _EXT = None
 
 

@@ -19,6 +19,19 @@ Usage::
     from fqkv_decode import hf_llama
     name = hf_llama.register()                 # "fqkv_decode"
     model.set_attn_implementation(name)        # or model.config._attn_implementation = name
+
+Quantized KV cache (no counterpart in the reference, whose hook keeps an fp16
+cache): :class:`QuantizedKVCache` stores every layer's keys and values in the
+int8 or int4 per-token format of ``fqkv_decode.quant``, quantizing new tokens
+with the GPU quantizer kernels, and the registered attention function runs
+decode steps on it with ``decode_attn_gqa_strided`` (the filled part of the
+preallocated cache is a strided view, read in place)::
+
+    cache = hf_llama.QuantizedKVCache(model.config, kv_format="int8")
+    model.generate(ids, past_key_values=cache, ...)
+
+The prompt's own prefill attends to its exact keys and values; a later call
+with more than one query token attends to the dequantized cache through SDPA.
 """
 
 import math
@@ -55,6 +68,8 @@ def kernel_applies(query, key, attention_mask, scaling, dropout, **kwargs):
 
 def attention_forward(module, query, key, value, attention_mask=None, scaling=None, dropout=0.0, **kwargs):
     """transformers attention function: query [B, Hq, q, D], key/value [B, Hkv, kv, D] -> ([B, q, Hq, D], None)."""
+    if getattr(key, "fqkv_scales", None) is not None:
+        return _quantized_attention(module, query, key, value, attention_mask, scaling, dropout, **kwargs)
     if getattr(module, "training", False) or not kernel_applies(query, key, attention_mask, scaling, dropout,
                                                                **kwargs):
         return _sdpa(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
@@ -65,6 +80,164 @@ def attention_forward(module, query, key, value, attention_mask=None, scaling=No
     V = value.to(torch.float16).contiguous()
     out = decode_attn_gqa(q, K, V, _W)                     # [B, Hq, D]
     return out.unsqueeze(1).to(query.dtype), None          # [B, 1, Hq, D]
+
+
+def _quantized_attention(module, query, key, value, attention_mask, scaling, dropout, **kwargs):
+    """Attention over a QuantizedKVCache view: key/value are int8 (or packed uint8) [B, Hkv, kv, D or D/2]
+    views carrying their fp16 scales [B, Hkv, kv] as ``fqkv_scales``."""
+    ks, vs = key.fqkv_scales, value.fqkv_scales
+    if not getattr(module, "training", False) and kernel_applies(query, key, attention_mask, scaling, dropout,
+                                                                 **kwargs):
+        from . import decode_attn_gqa_strided
+
+        q = query[:, :, 0, :].to(torch.float16).contiguous()
+        out = decode_attn_gqa_strided(q, key, value, _W, ks, vs)
+        return out.unsqueeze(1).to(query.dtype), None
+    from . import quant
+
+    deq = quant.dequant_int8 if key.dtype == torch.int8 else quant.dequant_int4
+    K = deq(key, ks).to(query.dtype)
+    V = deq(value, vs).to(query.dtype)
+    return _sdpa(module, query, K, V, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
+
+
+def _tag(view, scales):
+    view.fqkv_scales = scales
+    return view
+
+
+def _make_layer_class():
+    # built on first use, so importing this module does not import transformers
+    from transformers.cache_utils import DynamicLayer
+
+    class QuantizedKVLayer(DynamicLayer):
+        """One decoder layer's KV cache in the kernels' int8 / int4 per-token format.
+
+        Storage is preallocated [B, Hkv, capacity, D] int8 (or [.., D/2] packed
+        uint8 for int4) plus [B, Hkv, capacity] fp16 scales, grown in blocks of
+        ``block`` tokens; new tokens are quantized on the GPU (bytes identical
+        to ``fqkv_decode.quant``). ``keys`` / ``values`` are views of the filled
+        part. ``update`` returns the exact new states for a first (prefill)
+        call and the quantized views, tagged with their scales, afterwards.
+        """
+
+        def __init__(self, kv_format="int8", block=256):
+            super().__init__()
+            if kv_format not in ("int8", "int4"):
+                raise ValueError("kv_format must be 'int8' or 'int4', got %r" % (kv_format,))
+            self.kv_format = kv_format
+            self.block = block
+            self.length = 0
+            self._k = self._v = self._ks = self._vs = None
+
+        def lazy_initialization(self, key_states, value_states):
+            self.dtype, self.device = key_states.dtype, key_states.device
+            self.is_initialized = True
+
+        def _reserve(self, B, H, D, need):
+            cap = 0 if self._k is None else self._k.shape[2]
+            if need <= cap:
+                return
+            cap = -(-max(need, 2 * cap) // self.block) * self.block
+            width, dt = (D, torch.int8) if self.kv_format == "int8" else (D // 2, torch.uint8)
+            k = torch.empty(B, H, cap, width, dtype=dt, device=self.device)
+            v = torch.empty_like(k)
+            ks = torch.empty(B, H, cap, dtype=torch.float16, device=self.device)
+            vs = torch.empty_like(ks)
+            if self.length:
+                n = self.length
+                k[:, :, :n] = self._k[:, :, :n]
+                v[:, :, :n] = self._v[:, :, :n]
+                ks[:, :, :n] = self._ks[:, :, :n]
+                vs[:, :, :n] = self._vs[:, :, :n]
+            self._k, self._v, self._ks, self._vs = k, v, ks, vs
+
+        def _views(self):
+            n = self.length
+            self.keys, self.values = self._k[:, :, :n], self._v[:, :, :n]
+            return (_tag(self._k[:, :, :n], self._ks[:, :, :n]), _tag(self._v[:, :, :n], self._vs[:, :, :n]))
+
+        def update(self, key_states, value_states, *args, **kwargs):
+            from . import quantize_int4_per_token, quantize_int8_per_token
+
+            if not self.is_initialized:
+                self.lazy_initialization(key_states, value_states)
+            B, H, n, D = key_states.shape
+            first = self.length == 0
+            self._reserve(B, H, D, self.length + n)
+            quantize = quantize_int8_per_token if self.kv_format == "int8" else quantize_int4_per_token
+            src = (lambda t: t) if key_states.dtype in (torch.float16, torch.float32) else (lambda t: t.float())
+            kq, ks = quantize(src(key_states).contiguous())
+            vq, vs = quantize(src(value_states).contiguous())
+            pos = slice(self.length, self.length + n)
+            self._k[:, :, pos] = kq
+            self._v[:, :, pos] = vq
+            self._ks[:, :, pos] = ks
+            self._vs[:, :, pos] = vs
+            self.length += n
+            views = self._views()
+            return (key_states, value_states) if first else views
+
+        def get_seq_length(self):
+            return self.length
+
+        def get_max_length(self):
+            return -1
+
+        def crop(self, tokens_to_remove):
+            if tokens_to_remove > 0:  # legacy form: the length to keep
+                n = min(tokens_to_remove, self.length)
+            else:
+                n = self.length + tokens_to_remove
+            self.length = max(0, n)
+            if self._k is not None:
+                self._views()
+
+        def batch_repeat_interleave(self, repeats):
+            if self._k is not None:
+                self._k, self._v, self._ks, self._vs = (t.repeat_interleave(repeats, dim=0)
+                                                        for t in (self._k, self._v, self._ks, self._vs))
+                self._views()
+
+        def batch_select_indices(self, indices):
+            if self._k is not None:
+                self._k, self._v, self._ks, self._vs = (t[indices].contiguous()
+                                                        for t in (self._k, self._v, self._ks, self._vs))
+                self._views()
+
+        def reset(self):
+            self.length = 0
+            if self._k is not None:
+                self._views()
+
+        def offload(self):
+            raise NotImplementedError("QuantizedKVLayer does not support offloading")
+
+        def prefetch(self):
+            raise NotImplementedError("QuantizedKVLayer does not support offloading")
+
+    return QuantizedKVLayer
+
+
+_LAYER_CLASS = None
+
+
+def QuantizedKVLayer(kv_format="int8", block=256):
+    """A transformers cache layer holding int8 / int4 KV (class built on first use)."""
+    global _LAYER_CLASS
+    if _LAYER_CLASS is None:
+        _LAYER_CLASS = _make_layer_class()
+    return _LAYER_CLASS(kv_format, block)
+
+
+def QuantizedKVCache(config, kv_format="int8", block=256):
+    """A transformers ``Cache`` whose every layer is a :func:`QuantizedKVLayer`; pass it to
+    ``generate(past_key_values=...)`` or a forward call with the attention implementation
+    :func:`register` installed."""
+    from transformers.cache_utils import Cache
+
+    text = config.get_text_config(decoder=True) if hasattr(config, "get_text_config") else config
+    return Cache(layers=[QuantizedKVLayer(kv_format, block) for _ in range(text.num_hidden_layers)])
 
 
 def register(name=DEFAULT_NAME):

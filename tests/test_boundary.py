@@ -157,10 +157,14 @@ def test_capi_quantized_gqa_and_split_reject_bad_args(lib):
 
 def test_binding_exposes_quantized_and_quantizer_entry_points():
     for name in ("decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8", "gqa_sk_fast_int4",
-                 "quantize_int8_per_token", "quantize_int4_per_token"):
+                 "quantize_int8_per_token", "quantize_int4_per_token", "decode_attn_gqa_nhd",
+                 "decode_attn_gqa_strided", "decode_attn_gqa_paged"):
         assert callable(getattr(fqkv_decode, name))
     with pytest.raises(RuntimeError, match="^cuda"):
         fqkv_decode.quantize_int8_per_token(torch.zeros(4, 128))
+    K = torch.zeros(1, 2, 40, 64, dtype=torch.float16)[:, :, :30]
+    with pytest.raises(RuntimeError, match="^cuda"):
+        fqkv_decode.decode_attn_gqa_strided(torch.zeros(1, 4, 64, dtype=torch.float16), K, K, 8)
 
 
 def test_capi_layout_entry_points_reject_bad_args(lib):

@@ -133,3 +133,48 @@ def test_layout_entry_points_reject_bad_input():
     Ki = torch.zeros(1, 16, 2, 128, dtype=torch.int8, device="cuda")
     with pytest.raises(RuntimeError, match="^int8"):
         fq.decode_attn_gqa_nhd(q, Ki, Ki, 8)
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "int8", "int4"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_strided_view_of_a_larger_cache_equals_contiguous(fmt, D):
+    """decode_attn_gqa_strided on the filled part of a preallocated [B, Hkv, capacity, D]
+    cache gives the bytes of the contiguous entry point on a copy of that part."""
+    g = torch.Generator().manual_seed(52)
+    B, Hq, Hkv, N, cap = 2, 16, 4, 1234, 2048
+    q = draw(g, B, Hq, D).half().cuda()
+    if fmt == "fp16":
+        Kc, Vc = draw(g, B, Hkv, cap, D).half().cuda(), draw(g, B, Hkv, cap, D).half().cuda()
+        K, V = Kc[:, :, :N], Vc[:, :, :N]
+        a = fq.decode_attn_gqa(q, K.contiguous(), V.contiguous(), 8)
+        b = fq.decode_attn_gqa_strided(q, K, V, 8)
+    else:
+        Kc, Ksc, _ = quantize(fmt, draw(g, B, Hkv, cap, D))
+        Vc, Vsc, _ = quantize(fmt, draw(g, B, Hkv, cap, D))
+        K, V, Ks, Vs = Kc[:, :, :N], Vc[:, :, :N], Ksc[:, :, :N], Vsc[:, :, :N]
+        f = fq.decode_attn_gqa_int8 if fmt == "int8" else fq.decode_attn_gqa_int4
+        a = f(q, K.contiguous(), V.contiguous(), Ks.contiguous(), Vs.contiguous(), 8)
+        b = fq.decode_attn_gqa_strided(q, K, V, 8, Ks, Vs)
+    assert torch.equal(a, b)
+
+
+def test_strided_token_major_view_equals_nhd():
+    g = torch.Generator().manual_seed(53)
+    B, Hq, Hkv, N, D = 2, 32, 8, 700, 128
+    q = draw(g, B, Hq, D).half().cuda()
+    K, V = draw(g, B, N, Hkv, D).half().cuda(), draw(g, B, N, Hkv, D).half().cuda()
+    a = fq.decode_attn_gqa_nhd(q, K, V, 8)
+    b = fq.decode_attn_gqa_strided(q, K.transpose(1, 2), V.transpose(1, 2), 8)
+    assert torch.equal(a, b)
+
+
+def test_strided_rejects_bad_views():
+    q = torch.zeros(1, 4, 64, dtype=torch.float16, device="cuda")
+    K = torch.zeros(1, 2, 40, 64, dtype=torch.float16, device="cuda")
+    with pytest.raises(RuntimeError, match="^contig"):
+        fq.decode_attn_gqa_strided(q, K[..., ::2].expand(1, 2, 40, 32), K[..., ::2].expand(1, 2, 40, 32), 8)
+    with pytest.raises(RuntimeError, match="^shape"):
+        fq.decode_attn_gqa_strided(q, K, K[:, :, :30], 8)
+    with pytest.raises(RuntimeError, match="strides"):  # token stride not a multiple of 16 bytes
+        Kb = torch.zeros(1, 2, 40, 68, dtype=torch.float16, device="cuda")[..., :64]
+        fq.decode_attn_gqa_strided(q, Kb, Kb, 8)

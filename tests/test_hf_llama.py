@@ -7,7 +7,11 @@
   noise) and greedy generation token-for-token equal to SDPA's (a divergence
   is accepted only where SDPA's own top-2 logit margin is below 1e-2, i.e. at
   a numerical tie), at short and long context (the latter takes the
-  kernel's internal sequence split)."""
+  kernel's internal sequence split);
+* GPU, int8 / int4 KV cache (hf_llama.QuantizedKVCache): stored bytes equal
+  the quantizer's, attention over the cache view equals float32 attention
+  over the dequantized cache, decode logits equal SDPA over the same
+  dequantized cache, and generate() runs every decode step on the kernel."""
 
 import math
 
@@ -133,3 +137,105 @@ def test_gpu_decode_path_really_runs_the_kernel(monkeypatch):
     with torch.no_grad():
         model.generate(ids, max_new_tokens=3, do_sample=False)
     assert calls["n"] == 2 * 2  # 2 layers x 2 decode steps (the first token comes from prefill)
+
+
+# ------------------------------------------------------------ quantized KV cache ----
+
+def _prefill(model, ids, cache):
+    with torch.no_grad():
+        out = model(ids, past_key_values=cache, use_cache=True)
+    return out
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_gpu_quantized_cache_stores_the_quantizer_bytes(fmt):
+    """After a prefill, every layer holds exactly fqkv_decode.quant's bytes and scales of the
+    prompt's keys and values (the prefill itself attends to the exact states)."""
+    from fqkv_decode import quant
+
+    name = hf_llama.register()
+    model = tiny_llama(layers=2, dtype=torch.float16, device="cuda")
+    set_impl(model, name)
+    ids = torch.randint(0, 1000, (2, 300), generator=torch.Generator().manual_seed(4)).cuda()
+    dyn = transformers.DynamicCache(config=model.config)
+    ref_logits = _prefill(model, ids, dyn).logits
+    qc = hf_llama.QuantizedKVCache(model.config, fmt)
+    logits = _prefill(model, ids, qc).logits
+    assert torch.equal(logits, ref_logits)
+    assert qc.get_seq_length() == 300
+    qfn = quant.quant_int8_per_token if fmt == "int8" else quant.quant_int4_per_token
+    for lq, ld in zip(qc.layers, dyn.layers):
+        for got, gs, x in ((lq._k, lq._ks, ld.keys), (lq._v, lq._vs, ld.values)):
+            want, ws = qfn(x)
+            assert torch.equal(got[:, :, :300], want)
+            assert torch.equal(gs[:, :, :300], ws)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_gpu_quantized_cache_decode_step(fmt, monkeypatch):
+    """A decode step on the quantized cache. Attention level: the kernel on the strided
+    cache view equals float32 attention over the dequantized cache (max-abs 2e-3 relative
+    to the output scale). Model level: the logits equal those of SDPA over the same
+    dequantized cache to 2 % of the logit scale (SDPA sees fp16-rounded K/V), and, for
+    int8, stay within 15 % of the logit scale of an fp16 cache (quantization error)."""
+    import copy
+
+    from fqkv_decode import quant
+
+    name = hf_llama.register()
+    model = tiny_llama(dtype=torch.float16, device="cuda")
+    set_impl(model, name)
+    ids = torch.randint(0, 1000, (1, 1500), generator=torch.Generator().manual_seed(5)).cuda()
+    qc = hf_llama.QuantizedKVCache(model.config, fmt)
+    out = _prefill(model, ids, qc)
+    nxt = out.logits[:, -1:].argmax(-1)
+    qc2 = copy.deepcopy(qc)
+    with torch.no_grad():
+        got = model(nxt, past_key_values=qc, use_cache=True).logits.float()
+        monkeypatch.setattr(hf_llama, "kernel_applies", lambda *a, **k: False)
+        sdpa_deq = model(nxt, past_key_values=qc2, use_cache=True).logits.float()
+        monkeypatch.undo()
+        dyn = transformers.DynamicCache(config=model.config)
+        _prefill(model, ids, dyn)
+        fp16 = model(nxt, past_key_values=dyn, use_cache=True).logits.float()
+    assert qc.get_seq_length() == 1501
+    top = float(fp16.abs().max())
+    assert float((got - sdpa_deq).abs().max()) <= 0.02 * top
+    if fmt == "int8":
+        assert float((got - fp16).abs().max()) <= 0.15 * top
+
+    # attention level, layer 0, a fresh query
+    k, v = qc.layers[0]._views()
+    q = torch.randn(1, 8, 1, 64, device="cuda", generator=torch.Generator(device="cuda").manual_seed(0)).half()
+    o, _ = hf_llama.attention_forward(model.model.layers[0].self_attn, q, k, v, None, scaling=1 / 8)
+    deq = quant.dequant_int8 if fmt == "int8" else quant.dequant_int4
+    Kf = deq(k, k.fqkv_scales).float().repeat_interleave(4, 1)
+    Vf = deq(v, v.fqkv_scales).float().repeat_interleave(4, 1)
+    ref = torch.softmax(q.float() @ Kf.transpose(-1, -2) / 8, -1) @ Vf
+    err = float((o.float().transpose(1, 2) - ref).abs().max())
+    assert err <= 2e-3 * max(1.0, float(ref.abs().max())), (err, float(ref.abs().max()))
+
+
+@pytest.mark.gpu
+def test_gpu_generate_with_quantized_cache_runs_the_kernel(monkeypatch):
+    name = hf_llama.register()
+    model = tiny_llama(layers=2, dtype=torch.float16, device="cuda")
+    set_impl(model, name)
+    import fqkv_decode
+
+    calls = {"n": 0}
+    real = fqkv_decode.decode_attn_gqa_strided
+
+    def counting(*a, **k):
+        calls["n"] += 1
+        return real(*a, **k)
+
+    monkeypatch.setattr(fqkv_decode, "decode_attn_gqa_strided", counting, raising=False)
+    ids = torch.randint(0, 1000, (1, 20), generator=torch.Generator().manual_seed(6)).cuda()
+    with torch.no_grad():
+        out = model.generate(ids, max_new_tokens=300, do_sample=False,
+                             past_key_values=hf_llama.QuantizedKVCache(model.config, "int8", block=64))
+    assert out.shape == (1, 320)
+    assert calls["n"] == 2 * 299  # every decode step of both layers (the capacity grows past 256 on the way)
