@@ -508,4 +508,29 @@ int fqkv_quantize_kv(const void* X, int x_dtype, void* Q, void* scales, int64_t 
   return FQKV_OK;
 }
 
+int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, void* K_cache, void* V_cache,
+                            void* Ks_cache, void* Vs_cache, int64_t rows, int64_t n_new, int64_t capacity,
+                            int64_t pos, int64_t D, int kv_format, void* stream) {
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32)
+    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16 or FQKV_SRC_F32");
+  if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
+  if (rows < 1 || n_new < 1) return fail(FQKV_ERR_ARG, "rows and n_new must be >= 1, got %lld and %lld",
+                                         (long long)rows, (long long)n_new);
+  if (pos < 0 || capacity < 1 || n_new > capacity - pos)
+    return fail(FQKV_ERR_ARG, "pos: tokens %lld .. %lld do not fit a capacity of %lld", (long long)pos,
+                (long long)(pos + n_new - 1), (long long)capacity);
+  if (!K_new || !V_new || !K_cache || !V_cache || !Ks_cache || !Vs_cache) return fail(FQKV_ERR_ARG, "null tensor pointer");
+  const uintptr_t xal = (x_dtype == FQKV_SRC_F16 && D == 64) ? 8 : 16;
+  const uintptr_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
+  if (!aligned(K_new, xal) || !aligned(V_new, xal)) return fail(FQKV_ERR_ARG, "K_new and V_new must be %d-byte aligned", (int)xal);
+  if (!aligned(K_cache, qal) || !aligned(V_cache, qal)) return fail(FQKV_ERR_ARG, "caches must be %d-byte aligned", (int)qal);
+  if (!aligned(Ks_cache, 2) || !aligned(Vs_cache, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
+  hipError_t e = launch_quantize_append(x_dtype == FQKV_SRC_F16, kv_format, (int)D, K_new, V_new, K_cache, V_cache,
+                                        Ks_cache, Vs_cache, rows, n_new, capacity, pos, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "launch: quantize append kernel");
+  return FQKV_OK;
+}
+
 }  // extern "C"

@@ -100,5 +100,8 @@ hipError_t launch_dequant(int fmt, int D, int path, const void* Kq, const void* 
                           int64_t tokens, hipStream_t st);
 hipError_t launch_quantize(int src_f16, int fmt, int D, const void* X, void* Q, void* S, int64_t tokens,
                            hipStream_t st);
+hipError_t launch_quantize_append(int src_f16, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,
+                                  void* Sk, void* Sv, int64_t rows, int64_t n, int64_t cap, int64_t pos,
+                                  hipStream_t st);
 
 }  // namespace fqkv

@@ -21,6 +21,7 @@
 //
 // Layout: 16 lanes own one token row (D/16 consecutive elements each); a wave
 // covers 4 rows per step, a 256-thread workgroup 16, grid-striding over rows.
+// The append form writes a live cache's new K and V tokens in place.
 // The row maximum is a DPP all-reduce within the 16-lane row. HBM-bound:
 // reads 2 or 4 B per element, writes 1 or 0.5 B per element + 2 B per row.
 #include <hip/hip_runtime.h>
@@ -81,80 +82,107 @@ __device__ __forceinline__ void load_row_slice(const void* X, int64_t row, int i
   }
 }
 
+// Quantize source row `row` of X into destination row `dst` of Q / scales.
+// The calling 16 lanes stay active together (the DPP reduction spans them);
+// a group with live == false reads and writes nothing.
+template <bool F16, int QMAX, int D>
+__device__ __forceinline__ void quantize_row(const void* __restrict__ X, uint8_t* __restrict__ Q,
+                                             _Float16* __restrict__ scales, int64_t row, int64_t dst, bool live,
+                                             int i) {
+  constexpr int EPL = D / 16;  // elements per lane
+  float x[EPL];
+  if (live) {
+    load_row_slice<F16, EPL>(X, row, i, D, x);
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) x[e] = 0.0f;
+  }
+  float a = 0.0f;
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) a = fmaxf(a, fabsf(x[e]));
+  a = row16_max(a);
+
+  float s;          // the divisor, as the reference holds it
+  _Float16 s_out;   // the stored scale
+  if constexpr (F16) {
+    s_out = (_Float16)(a * (1.0f / (float)QMAX));  // fp16 op: fp32 result rounded to fp16
+    s = (float)s_out;                      // clamp(min=1e-8) cannot lift an fp16 value
+  } else {
+    s = fmaxf(a * (1.0f / (float)QMAX), 1e-8f);
+    s_out = (_Float16)s;
+  }
+  int q[EPL];
+#pragma unroll
+  for (int e = 0; e < EPL; ++e) {
+    float quot;
+    if constexpr (F16) {
+      if (s == 0.0f) {
+        quot = x[e] == 0.0f ? 0.0f : copysignf((float)QMAX, x[e]);
+      } else {
+        quot = (float)(_Float16)(x[e] / s);
+      }
+    } else {
+      quot = x[e] / s;
+    }
+    const float r = fminf(fmaxf(__builtin_rintf(quot), -(float)QMAX), (float)QMAX);
+    q[e] = (int)r;
+  }
+  if (!live) return;
+  if constexpr (QMAX == 127) {
+    uint32_t w[EPL / 4];
+#pragma unroll
+    for (int k = 0; k < EPL / 4; ++k)
+      w[k] = (uint32_t)(q[4 * k] & 0xFF) | ((uint32_t)(q[4 * k + 1] & 0xFF) << 8) |
+             ((uint32_t)(q[4 * k + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * k + 3] & 0xFF) << 24);
+    uint8_t* out = Q + dst * D + EPL * i;
+    if constexpr (EPL == 8) {
+      *(u2_t*)out = u2_t{w[0], w[1]};
+    } else {
+      *(uint32_t*)out = w[0];
+    }
+  } else {
+    uint32_t w = 0;
+#pragma unroll
+    for (int t = 0; t < EPL / 2; ++t)
+      w |= ((uint32_t)(q[2 * t] & 0xF) | ((uint32_t)(q[2 * t + 1] & 0xF) << 4)) << (8 * t);
+    uint8_t* out = Q + dst * (D / 2) + (EPL / 2) * i;
+    if constexpr (EPL == 8) {
+      *(uint32_t*)out = w;
+    } else {
+      *(uint16_t*)out = (uint16_t)w;
+    }
+  }
+  if (i == 0) scales[dst] = s_out;
+}
+
 template <bool F16, int QMAX, int D>
 __global__ void __launch_bounds__(256) quantize_kernel(const void* __restrict__ X, uint8_t* __restrict__ Q,
                                                        _Float16* __restrict__ scales, int64_t tokens) {
-  constexpr int EPL = D / 16;  // elements per lane
   const int i = threadIdx.x & 15;
   const int64_t rows_per_step = (int64_t)gridDim.x * (blockDim.x >> 4);
   for (int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
-       row - (threadIdx.x >> 4) < tokens; row += rows_per_step) {
-    // whole 16-lane rows stay active through the DPP reduction; a row past
-    // the end reads nothing and stores nothing
-    const bool live = row < tokens;
-    float x[EPL];
-    if (live) {
-      load_row_slice<F16, EPL>(X, row, i, D, x);
-    } else {
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) x[e] = 0.0f;
-    }
-    float a = 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) a = fmaxf(a, fabsf(x[e]));
-    a = row16_max(a);
+       row - (threadIdx.x >> 4) < tokens; row += rows_per_step)
+    quantize_row<F16, QMAX, D>(X, Q, scales, row, row, row < tokens, i);
+}
 
-    float s;          // the divisor, as the reference holds it
-    _Float16 s_out;   // the stored scale
-    if constexpr (F16) {
-      s_out = (_Float16)(a * (1.0f / (float)QMAX));  // fp16 op: fp32 result rounded to fp16
-      s = (float)s_out;                      // clamp(min=1e-8) cannot lift an fp16 value
-    } else {
-      s = fmaxf(a * (1.0f / (float)QMAX), 1e-8f);
-      s_out = (_Float16)s;
-    }
-    int q[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      float quot;
-      if constexpr (F16) {
-        if (s == 0.0f) {
-          quot = x[e] == 0.0f ? 0.0f : copysignf((float)QMAX, x[e]);
-        } else {
-          quot = (float)(_Float16)(x[e] / s);
-        }
-      } else {
-        quot = x[e] / s;
-      }
-      const float r = fminf(fmaxf(__builtin_rintf(quot), -(float)QMAX), (float)QMAX);
-      q[e] = (int)r;
-    }
-    if (!live) continue;
-    if constexpr (QMAX == 127) {
-      uint32_t w[EPL / 4];
-#pragma unroll
-      for (int k = 0; k < EPL / 4; ++k)
-        w[k] = (uint32_t)(q[4 * k] & 0xFF) | ((uint32_t)(q[4 * k + 1] & 0xFF) << 8) |
-               ((uint32_t)(q[4 * k + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * k + 3] & 0xFF) << 24);
-      uint8_t* dst = Q + row * D + EPL * i;
-      if constexpr (EPL == 8) {
-        *(u2_t*)dst = u2_t{w[0], w[1]};
-      } else {
-        *(uint32_t*)dst = w[0];
-      }
-    } else {
-      uint32_t w = 0;
-#pragma unroll
-      for (int t = 0; t < EPL / 2; ++t)
-        w |= ((uint32_t)(q[2 * t] & 0xF) | ((uint32_t)(q[2 * t + 1] & 0xF) << 4)) << (8 * t);
-      uint8_t* dst = Q + row * (D / 2) + (EPL / 2) * i;
-      if constexpr (EPL == 8) {
-        *(uint32_t*)dst = w;
-      } else {
-        *(uint16_t*)dst = (uint16_t)w;
-      }
-    }
-    if (i == 0) scales[row] = s_out;
+// Append form for a live cache: K and V rows of `rows` cache rows x n new
+// tokens ([rows, n, D] each, contiguous) go to token positions pos .. pos+n-1
+// of caches laid out [rows, cap, D or D/2] with scales [rows, cap]. One launch
+// covers both tensors: row index j < rows*n is K, the rest V.
+template <bool F16, int QMAX, int D>
+__global__ void __launch_bounds__(256) quantize_append_kernel(const void* __restrict__ Xk, const void* __restrict__ Xv,
+                                                              uint8_t* __restrict__ Qk, uint8_t* __restrict__ Qv,
+                                                              _Float16* __restrict__ Sk, _Float16* __restrict__ Sv,
+                                                              int64_t tokens, int64_t n, int64_t cap, int64_t pos) {
+  const int i = threadIdx.x & 15;
+  const int64_t rows_per_step = (int64_t)gridDim.x * (blockDim.x >> 4);
+  for (int64_t j = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
+       j - (threadIdx.x >> 4) < 2 * tokens; j += rows_per_step) {
+    const bool v = j >= tokens;
+    const int64_t row = v ? j - tokens : j;
+    const int64_t r = row / n;
+    quantize_row<F16, QMAX, D>(v ? Xv : Xk, v ? Qv : Qk, v ? Sv : Sk, row, r * cap + pos + (row - r * n),
+                               j < 2 * tokens, i);
   }
 }
 
@@ -171,7 +199,35 @@ hipError_t launch_q(int D, const void* X, void* Q, void* S, int64_t tokens, hipS
   return hipGetLastError();
 }
 
+template <bool F16, int QMAX>
+hipError_t launch_qa(int D, const void* Xk, const void* Xv, void* Qk, void* Qv, void* Sk, void* Sv, int64_t tokens,
+                     int64_t n, int64_t cap, int64_t pos, hipStream_t st) {
+  const int64_t want = (2 * tokens + 15) / 16;
+  const unsigned grid = (unsigned)(want < (1 << 16) ? want : (1 << 16));
+  if (D == 128)
+    hipLaunchKernelGGL((quantize_append_kernel<F16, QMAX, 128>), dim3(grid), dim3(256), 0, st, Xk, Xv,
+                       (uint8_t*)Qk, (uint8_t*)Qv, (_Float16*)Sk, (_Float16*)Sv, tokens, n, cap, pos);
+  else
+    hipLaunchKernelGGL((quantize_append_kernel<F16, QMAX, 64>), dim3(grid), dim3(256), 0, st, Xk, Xv,
+                       (uint8_t*)Qk, (uint8_t*)Qv, (_Float16*)Sk, (_Float16*)Sv, tokens, n, cap, pos);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+hipError_t launch_quantize_append(int src_f16, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,
+                                  void* Sk, void* Sv, int64_t rows, int64_t n, int64_t cap, int64_t pos,
+                                  hipStream_t st) {
+  if (rows < 1 || n < 1 || cap < 1 || pos < 0 || pos + n > cap || (D != 64 && D != 128)) return hipErrorInvalidValue;
+  const int64_t tokens = rows * n;
+  if (fmt == KV_I8)
+    return src_f16 ? launch_qa<true, 127>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, st)
+                   : launch_qa<false, 127>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, st);
+  if (fmt == KV_I4)
+    return src_f16 ? launch_qa<true, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, st)
+                   : launch_qa<false, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, st);
+  return hipErrorInvalidValue;
+}
 
 hipError_t launch_quantize(int src_f16, int fmt, int D, const void* X, void* Q, void* S, int64_t tokens,
                            hipStream_t st) {

@@ -530,6 +530,38 @@ static std::vector<torch::Tensor> quantize_int4_per_token(torch::Tensor X) {
   return quantize_per_token(X, FQKV_KV_I4);
 }
 
+// quantize_kv_append_(K_new[B,H,n,D], V_new, K_cache[B,H,cap,D or D/2], V_cache, Ks_cache[B,H,cap],
+// Vs_cache, pos) -> None: quantizes the new tokens into cache positions pos .. pos+n-1 in place.
+static void quantize_kv_append(torch::Tensor Kn, torch::Tensor Vn, torch::Tensor Kc, torch::Tensor Vc,
+                               torch::Tensor Ksc, torch::Tensor Vsc, int64_t pos) {
+  check_gpu({&Kn, &Vn, &Kc, &Vc, &Ksc, &Vsc});
+  TORCH_CHECK(Kn.scalar_type() == torch::kHalf || Kn.scalar_type() == torch::kFloat,
+              "fp16: K_new must be float16 or float32");
+  TORCH_CHECK(Vn.scalar_type() == Kn.scalar_type() && Vn.sizes() == Kn.sizes() && Kn.dim() == 4,
+              "shape: K_new and V_new must be [B,H,n,D] of one dtype; got ", Kn.sizes(), " and ", Vn.sizes());
+  TORCH_CHECK(Kc.scalar_type() == torch::kChar || Kc.scalar_type() == torch::kByte,
+              "int8: caches must be int8 or packed uint8 (int4)");
+  const int fmt = Kc.scalar_type() == torch::kChar ? FQKV_KV_I8 : FQKV_KV_I4;
+  const int64_t B = Kn.size(0), H = Kn.size(1), n = Kn.size(2), D = Kn.size(3);
+  check_D(D);
+  TORCH_CHECK(Kc.dim() == 4 && Kc.size(0) == B && Kc.size(1) == H && Kc.size(3) == (fmt == FQKV_KV_I8 ? D : D / 2) &&
+                  Vc.sizes() == Kc.sizes() && Vc.scalar_type() == Kc.scalar_type(),
+              "shape: caches must be [B,H,capacity,", fmt == FQKV_KV_I8 ? "D" : "D/2", "] matching K_new ", Kn.sizes(),
+              "; got ", Kc.sizes(), " and ", Vc.sizes());
+  const int64_t cap = Kc.size(2);
+  check_half(Ksc, "Ks_cache");
+  check_half(Vsc, "Vs_cache");
+  TORCH_CHECK(Ksc.sizes() == at::IntArrayRef({B, H, cap}) && Vsc.sizes() == Ksc.sizes(),
+              "shape: scale caches must be [B,H,capacity] = [", B, ",", H, ",", cap, "]; got ", Ksc.sizes(), " and ",
+              Vsc.sizes());
+  const c10::DeviceGuard guard(Kn.device());
+  check_rc(fqkv_quantize_kv_append(Kn.data_ptr(), Vn.data_ptr(),
+                                   Kn.scalar_type() == torch::kHalf ? FQKV_SRC_F16 : FQKV_SRC_F32, Kc.data_ptr(),
+                                   Vc.data_ptr(), Ksc.data_ptr(), Vsc.data_ptr(), B * H, n, cap, pos, D, fmt,
+                                   cur_stream(Kn)),
+           "launch");
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "MI355X fused single-query decode attention (fp16 / int8-KV / int4-KV / GQA / GQA split-K)";
   m.def("decode_attn_fp16_mw", &decode_attn_fp16_mw, "fp16 fused decode", py::arg("q"), py::arg("K"), py::arg("V"),
@@ -568,6 +600,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "per-token int8 KV quantizer on the GPU -> (int8 [..., D], fp16 scales [...])", py::arg("X"));
   m.def("quantize_int4_per_token", &quantize_int4_per_token,
         "per-token int4 KV quantizer on the GPU -> (packed uint8 [..., D/2], fp16 scales [...])", py::arg("X"));
+  m.def("quantize_kv_append_", &quantize_kv_append,
+        "quantize new K/V tokens [B,H,n,D] into int8 / int4 caches [B,H,capacity,.] at position pos, in place",
+        py::arg("K_new"), py::arg("V_new"), py::arg("K_cache"), py::arg("V_cache"), py::arg("Ks_cache"),
+        py::arg("Vs_cache"), py::arg("pos"));
   m.def("_choose_splits", &choose_splits, "split count the single-block entry points use");
   m.def("_cu_count", &cu_count, "compute units of the current device");
   m.def("_version", []() { return std::string(fqkv_version()); });

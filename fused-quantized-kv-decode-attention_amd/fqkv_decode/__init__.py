@@ -18,6 +18,9 @@ Beyond the reference (same conventions, no counterpart there):
         m_part, l_part, o_part, o, S, W, CW)        split-K over an int8 / int4 cache
     quantize_int8_per_token / quantize_int4_per_token(X[..., D]) -> (bytes, fp16 scales)
                                                     the KV quantizers as GPU kernels
+    quantize_kv_append_(K_new[B,H,n,D], V_new, K_cache[B,H,cap,D or D/2], V_cache,
+        Ks_cache[B,H,cap], Vs_cache, pos) -> None  the quantizers in append form for a live
+                                                    cache: one launch, in place at pos
     decode_attn_gqa_nhd(q[B,Hq,D], K[B,N,Hkv,D], V, W, Ks=None, Vs=None) -> o[B,Hq,D]
                                                     token-major (FlashInfer NHD) KV layout
     decode_attn_gqa_strided(q[B,Hq,D], K[B,Hkv,N,D] view, V, W, Ks=None, Vs=None) -> o[B,Hq,D]
@@ -55,6 +58,7 @@ __all__ = [
     "gqa_sk_fast_int4",
     "quantize_int8_per_token",
     "quantize_int4_per_token",
+    "quantize_kv_append_",
     "decode_attn_gqa_nhd",
     "decode_attn_gqa_strided",
     "decode_attn_gqa_paged",
@@ -65,7 +69,7 @@ __all__ = [
 
 _ENTRY_POINTS = ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa",
                  "gqa_sk_fast", "decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8",
-                 "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token",
+                 "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token", "quantize_kv_append_",
                  "decode_attn_gqa_nhd", "decode_attn_gqa_strided", "decode_attn_gqa_paged")
 _EXT = None
 

@@ -115,8 +115,9 @@ def _make_layer_class():
 
         Storage is preallocated [B, Hkv, capacity, D] int8 (or [.., D/2] packed
         uint8 for int4) plus [B, Hkv, capacity] fp16 scales, grown in blocks of
-        ``block`` tokens; new tokens are quantized on the GPU (bytes identical
-        to ``fqkv_decode.quant``). ``keys`` / ``values`` are views of the filled
+        ``block`` tokens; new tokens are quantized on the GPU straight into
+        their slots (``quantize_kv_append_``, bytes identical to
+        ``fqkv_decode.quant``). ``keys`` / ``values`` are views of the filled
         part. ``update`` returns the exact new states for a first (prefill)
         call and the quantized views, tagged with their scales, afterwards.
         """
@@ -158,22 +159,17 @@ def _make_layer_class():
             return (_tag(self._k[:, :, :n], self._ks[:, :, :n]), _tag(self._v[:, :, :n], self._vs[:, :, :n]))
 
         def update(self, key_states, value_states, *args, **kwargs):
-            from . import quantize_int4_per_token, quantize_int8_per_token
+            from . import quantize_kv_append_
 
             if not self.is_initialized:
                 self.lazy_initialization(key_states, value_states)
             B, H, n, D = key_states.shape
             first = self.length == 0
             self._reserve(B, H, D, self.length + n)
-            quantize = quantize_int8_per_token if self.kv_format == "int8" else quantize_int4_per_token
             src = (lambda t: t) if key_states.dtype in (torch.float16, torch.float32) else (lambda t: t.float())
-            kq, ks = quantize(src(key_states).contiguous())
-            vq, vs = quantize(src(value_states).contiguous())
-            pos = slice(self.length, self.length + n)
-            self._k[:, :, pos] = kq
-            self._v[:, :, pos] = vq
-            self._ks[:, :, pos] = ks
-            self._vs[:, :, pos] = vs
+            # one launch quantizes the new K and V tokens into their cache slots
+            quantize_kv_append_(src(key_states).contiguous(), src(value_states).contiguous(), self._k, self._v,
+                                self._ks, self._vs, self.length)
             self.length += n
             views = self._views()
             return (key_states, value_states) if first else views

@@ -228,6 +228,21 @@ int fqkv_quantize_kv(const void* X, int x_dtype, void* Q, void* scales, int64_t 
                      int kv_format, void* stream);
 
 /*
+ * The quantizer above in append form, for a live decode cache: the new keys
+ * and values K_new, V_new [rows, n_new, D] (fp16 or fp32, contiguous) are
+ * quantized in one launch into token positions pos .. pos + n_new - 1 of the
+ * caches K_cache, V_cache [rows, capacity, D] int8 (or [.., D/2] packed
+ * uint8) with scales Ks_cache, Vs_cache [rows, capacity] fp16, all
+ * contiguous; rows = batch * kv_heads. The bytes equal fqkv_quantize_kv's on
+ * the same tokens; nothing else in the caches changes. No counterpart in the
+ * reference (its quantizers run on the CPU over whole tensors,
+ * tests/test_kernels.py:32-34, nb:292-299).
+ */
+int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, void* K_cache, void* V_cache,
+                            void* Ks_cache, void* Vs_cache, int64_t rows, int64_t n_new, int64_t capacity,
+                            int64_t pos, int64_t D, int kv_format, void* stream);
+
+/*
  * Split merge mode for calls that split the sequence (gqa_sk_fast with S > 1
  * and the internal splits of the single-block entry points). Default (0):
  * one kernel per call; the last workgroup of each head group to finish merges

@@ -142,6 +142,19 @@ def test_capi_quantizer_rejects_bad_args(lib):
     assert f(16, 1, 20, 16, 4, 128, 1, None) == 1 and "aligned" in _err(lib)
 
 
+def test_capi_quantize_append_rejects_bad_args(lib):
+    f = lib.fqkv_quantize_kv_append
+    f.argtypes = [VP, VP, ctypes.c_int] + [VP] * 4 + [I64] * 5 + [ctypes.c_int, VP]
+    ok = [16, 16, 1, 16, 16, 16, 16]
+    assert f(*ok, 8, 2, 100, 99, 128, 1, None) == 1 and _err(lib).startswith("pos:")
+    assert f(*ok, 8, 1, 100, -1, 128, 1, None) == 1 and _err(lib).startswith("pos:")
+    assert f(*ok, 8, 0, 100, 0, 128, 1, None) == 1 and "n_new" in _err(lib)
+    assert f(*ok, 8, 1, 100, 0, 128, 0, None) == 1 and "kv_format" in _err(lib)
+    assert f(*ok, 8, 1, 100, 0, 96, 1, None) == 1 and _err(lib).startswith("D:")
+    assert f(16, None, 1, 16, 16, 16, 16, 8, 1, 100, 0, 128, 1, None) == 1 and "null" in _err(lib)
+    assert f(16, 16, 1, 20, 16, 16, 16, 8, 1, 100, 0, 128, 1, None) == 1 and "aligned" in _err(lib)
+
+
 def test_capi_quantized_gqa_and_split_reject_bad_args(lib):
     fg = lib.fqkv_decode_attn_gqa_quant
     fg.argtypes = [VP] * 6 + [I64] * 5 + [ctypes.c_int, I64, VP, ctypes.c_size_t, VP]

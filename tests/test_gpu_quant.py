@@ -98,3 +98,36 @@ def test_gpu_quantizer_rejects_bad_input():
         fq.quantize_int4_per_token(torch.zeros(4, 64, device="cuda", dtype=torch.float64))
     with pytest.raises(RuntimeError, match="^contig:"):
         fq.quantize_int8_per_token(torch.zeros(64, 4, device="cuda").t())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_gpu_quantize_append_writes_only_its_slots(dtype, D, fmt):
+    """quantize_kv_append_ puts the quantizer's bytes and scales of the new K and V
+    tokens at positions pos .. pos+n-1 of every cache row and leaves the rest alone."""
+    B, H, cap = 2, 3, 40
+    g = torch.Generator().manual_seed(60)
+    width, qdt = (D, torch.int8) if fmt == "int8" else (D // 2, torch.uint8)
+    Kc = torch.full((B, H, cap, width), 0x55, dtype=qdt, device="cuda")
+    Vc = torch.full_like(Kc, 0x33)
+    Ksc = torch.full((B, H, cap), 7.0, dtype=torch.float16, device="cuda")
+    Vsc = torch.full_like(Ksc, 9.0)
+    qfn = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+    pos = 0
+    for n in (5, 1, 1, 17):
+        Kn = (torch.randn(B, H, n, D, generator=g) * 3).to(dtype).cuda()
+        Vn = (torch.randn(B, H, n, D, generator=g) * 3).to(dtype).cuda()
+        if n == 17:
+            Kn[0, 0, 0] = torch.from_numpy(edge_rows(D, np.float16 if dtype == torch.float16 else np.float32)[1])
+        before = [t.clone() for t in (Kc, Vc, Ksc, Vsc)]
+        fq.quantize_kv_append_(Kn, Vn, Kc, Vc, Ksc, Vsc, pos)
+        for got, old, (q, s) in ((Kc, before[0], qfn(Kn)), (Vc, before[1], qfn(Vn))):
+            assert torch.equal(got[:, :, pos:pos + n], q)
+            assert torch.equal(got[:, :, :pos], old[:, :, :pos]) and torch.equal(got[:, :, pos + n:], old[:, :, pos + n:])
+        for got, old, (q, s) in ((Ksc, before[2], qfn(Kn)), (Vsc, before[3], qfn(Vn))):
+            assert torch.equal(got[:, :, pos:pos + n], s)
+            assert torch.equal(got[:, :, :pos], old[:, :, :pos]) and torch.equal(got[:, :, pos + n:], old[:, :, pos + n:])
+        pos += n
+    with pytest.raises(RuntimeError, match="pos"):
+        fq.quantize_kv_append_(Kn[:, :, :1].contiguous(), Vn[:, :, :1].contiguous(), Kc, Vc, Ksc, Vsc, cap)
