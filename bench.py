@@ -238,11 +238,17 @@ def _ref_mha(torch, q, Kf, Vf):
     return torch.bmm(torch.softmax(s, dim=1).unsqueeze(1), Vf).squeeze(1)
 
 
+# The reference's A100 results at its own precision shape (D 64, N 4096, W 8): fp16 / int8 / int4
+# ms per call (benchmarks/standalone_quant.json:6-34; per-call events, synchronised).
+REF_QUANT_D64_MS = {8: (0.2263, 0.2478, 0.2662), 256: (0.4792, 0.4864, 0.4915), 2048: (2.0951, 1.6814, 1.5585)}
+
+
 def suite_mha_quant(torch, fq, steps, warmup, rows):
-    """fp16 / int8 / int4 MHA decode at B in {8, 256, 2048}, N=4096, D=128, W=8."""
+    """fp16 / int8 / int4 MHA decode at B in {8, 256, 2048}, N=4096, W=8, at D=128 and at the
+    reference's own D=64 (its A100 numbers alongside)."""
     from fqkv_decode import quant
-    N, Dm, W = 4096, 128, 8
-    for B in (8, 256, 2048):
+    N, W = 4096, 8
+    for Dm, B in [(128, b) for b in (8, 256, 2048)] + [(64, b) for b in (8, 256, 2048)]:
         g = torch.Generator(device="cuda").manual_seed(1)
         q = torch.randn(B, Dm, device="cuda", generator=g).half()
         per = {"fp16": 2 * B * N * Dm * 2, "int8": 2 * B * N * Dm + 4 * B * N, "int4": B * N * Dm + 4 * B * N}
@@ -285,17 +291,26 @@ def suite_mha_quant(torch, fq, steps, warmup, rows):
             err = float((o.float() - ref).abs().max())
             del Kf, Vf, ref
             ms = _loop_ms(torch, fn, ns, steps, warmup)
-            rows.append(_row("mha_" + fmt, {"B": B, "N": N, "D": Dm, "W": W, "sets": ns}, ms, nbytes, err))
+            extra = {}
+            if Dm == 64:
+                extra = {"ref_a100_us": REF_QUANT_D64_MS[B][("fp16", "int8", "int4").index(fmt)] * 1e3}
+            rows.append(_row("mha_" + fmt, {"B": B, "N": N, "D": Dm, "W": W, "sets": ns}, ms, nbytes, err, **extra))
             log("%-10s B=%-5d N=%d D=%d  %9.2f us  %7.1f GB/s  err %.2e" % (fmt, B, N, Dm, ms * 1e3, nbytes / ms / 1e6, err))
             del sets
             torch.cuda.empty_cache()
 
 
+# The reference's A100 results at its own GQA shape (Hq 32, Hkv 8, D 64, N 4096, W 8):
+# GQA-aware ms and repeat_kv + MHA ms per batch (benchmarks/gqa_aware.json:2-24).
+REF_GQA_N4096_MS = {1: (0.2417, 0.5898), 4: (0.4588, 0.8735), 16: (0.4506, 1.6148)}
+
+
 def suite_gqa(torch, fq, steps, warmup, rows):
-    """decode_attn_gqa vs repeat_kv + MHA kernel: Hq=32, Hkv=8, D=64, N=512, B in {1,4,16}."""
-    Hq, Hkv, N, Dg, W = 32, 8, 512, 64, 8
+    """decode_attn_gqa vs repeat_kv + MHA kernel: Hq=32, Hkv=8, D=64, B in {1,4,16}, at N=512
+    and at the reference's own N=4096 (its A100 numbers alongside)."""
+    Hq, Hkv, Dg, W = 32, 8, 64, 8
     G = Hq // Hkv
-    for B in (1, 4, 16):
+    for N, B in [(512, b) for b in (1, 4, 16)] + [(4096, b) for b in (1, 4, 16)]:
         g = torch.Generator(device="cuda").manual_seed(2)
         per = 2 * B * Hkv * N * Dg * 2
         ns = _nsets(per)
@@ -318,8 +333,11 @@ def suite_gqa(torch, fq, steps, warmup, rows):
             return fq.decode_attn_fp16_mw(qf, Ke, Ve, W)
 
         ms_x = _loop_ms(torch, expand, ns, steps, warmup)
+        extra = {}
+        if N == 4096:
+            extra = {"ref_a100_gqa_us": REF_GQA_N4096_MS[B][0] * 1e3, "ref_a100_expand_us": REF_GQA_N4096_MS[B][1] * 1e3}
         rows.append(_row("gqa", {"B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": Dg, "W": W, "sets": ns}, ms, nbytes, err,
-                         expand_mha_us=round(ms_x * 1e3, 3), speedup_vs_expand=round(ms_x / ms, 3)))
+                         expand_mha_us=round(ms_x * 1e3, 3), speedup_vs_expand=round(ms_x / ms, 3), **extra))
         log("gqa       B=%-3d N=%d D=%d  %8.2f us (repeat_kv + MHA %8.2f us, %.2fx)  err %.2e"
             % (B, N, Dg, ms * 1e3, ms_x * 1e3, ms_x / ms, err))
         del sets, Kf, Vf
