@@ -200,3 +200,30 @@ def test_cabi_quantized_gqa_and_split(lib, fmt):
     torch.cuda.synchronize()
     assert maxerr(o, ref) <= TOL
     assert maxerr(o2, ref[0]) <= TOL
+
+
+def test_plain_c_caller(tmp_path):
+    """tests/c_abi_caller.c, a C program with no Python or PyTorch, built with gcc against
+    include/fqkv_decode.h and libfqkv_decode.so, runs fqkv_gqa_sk_fast and
+    fqkv_decode_attn_gqa on its own device buffers and checks them against a host reference."""
+    import os
+    import shutil
+    import subprocess
+
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("gcc not found")
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    pkg = os.path.dirname(fqkv_decode.lib_path())
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    exe = str(tmp_path / "c_abi_caller")
+    build = subprocess.run([gcc, "-O2", "-std=c11", "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(root, "include"),
+                            "-I", os.path.join(rocm, "include"), os.path.join(here, "c_abi_caller.c"), "-o", exe,
+                            "-L", pkg, "-lfqkv_decode", "-L", os.path.join(rocm, "lib"), "-lamdhip64",
+                            "-Wl,-rpath," + pkg + ":" + os.path.join(rocm, "lib"), "-lm"],
+                           capture_output=True, text=True)
+    assert build.returncode == 0, build.stderr
+    run = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert run.returncode == 0, run.stdout + run.stderr
+    assert run.stdout.strip().splitlines()[-1].startswith("OK"), run.stdout
