@@ -103,13 +103,28 @@ typedef float fl4_t __attribute__((ext_vector_type(4)));
 
 // Arrival counters of the in-kernel split merge. Zero at load; the workgroup
 // that merges a group resets its counter, so every call leaves them at zero.
-__device__ int g_split_arrivals[SPLIT_SLOTS][MAX_SPLIT_GROUPS];
+// Device-scope atomics on one cache line serialise, so the counters of
+// consecutive groups sit 256 bytes apart (group g of a slot at int
+// (g % 256) * 64 + g / 256): with them packed, every workgroup of a call
+// queued on the same one or two lines, and the merge's cost moved with the
+// array's alignment. 256-byte alignment keeps the lines of different groups
+// apart.
+constexpr int ARRIVAL_LINES = 256;
+static_assert(MAX_SPLIT_GROUPS % ARRIVAL_LINES == 0 && MAX_SPLIT_GROUPS / ARRIVAL_LINES <= 64,
+              "arrival counters: at most 64 per 256-byte line");
+__device__ __attribute__((aligned(256))) int g_split_arrivals[SPLIT_SLOTS][MAX_SPLIT_GROUPS];
+__device__ __forceinline__ int* arrival_counter(int slot, uint32_t group) {
+  return &g_split_arrivals[slot][(group % ARRIVAL_LINES) * 64 + group / ARRIVAL_LINES];
+}
 
 // Full-wave reductions: DPP within each 16-lane row (quad_perm [1,0,3,2],
 // quad_perm [2,3,0,1], row_half_mirror, row_mirror), then across the rows.
+// Every pattern used here reads a lane of the same row, so bound_ctrl (zero
+// for a source outside the row) never applies; setting it lets the compiler
+// fold the move into the consuming add (v_add_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float wave_max(float x) {
   x = fmaxf(x, dpp_f<0xB1>(x));
@@ -124,6 +139,56 @@ __device__ __forceinline__ float wave_sum(float x) {
   x += dpp_f<0x141>(x);
   x += dpp_f<0x140>(x);
   return rows4_sum(x);
+}
+
+// Column packing of the score product. A 16 x 16 score tile has 16 head
+// columns but a work item has only HG query heads, so P = min(U, 16 / HG)
+// tiles of a pass share one column set: column n holds head n % HG of tile
+// n / HG of each group of P tiles. cols_reduce combines the P columns of each
+// head within a 16-lane row (DPP quad_perm xor 1 / xor 2, row_ror 4 / 8);
+// columns past P * HG take part only in HG = 2 and must hold a neutral value
+// (or, for a maximum, any value of the same pass).
+template <int HG, int P, bool MAX>
+__device__ __forceinline__ float cols_reduce(float x) {
+  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+  if constexpr (P == 1) {
+    return x;
+  } else if constexpr (HG == 1) {  // columns 0..3: one quad
+    x = op(x, dpp_f<0xB1>(x));
+    return op(x, dpp_f<0x4E>(x));
+  } else if constexpr (HG == 2) {  // columns hh, hh + 2, hh + 4, hh + 6
+    x = op(x, dpp_f<0x4E>(x));
+    x = op(x, dpp_f<0x124>(x));
+    return op(x, dpp_f<0x128>(x));
+  } else if constexpr (HG == 4) {  // columns hh + 4 j, j = 0..3
+    x = op(x, dpp_f<0x124>(x));
+    return op(x, dpp_f<0x128>(x));
+  } else {  // HG == 8, P == 2: columns hh, hh + 8
+    static_assert(HG == 8 && P == 2, "column packing");
+    return op(x, dpp_f<0x128>(x));
+  }
+}
+
+// f(jl) for the lane's tile index jl < P. The selects are bitwise blends
+// under the loop-invariant lane masks m1 = -(jl & 1), m2 = -((jl >> 1) & 1)
+// (one v_bfi_b32 each): written as conditionals, the compiler turns the
+// chain into a per-lane indexed array in scratch memory.
+template <typename T>
+__device__ __forceinline__ T blend(uint32_t m, T a, T b) {  // m ? b : a
+  static_assert(sizeof(T) == 4, "32-bit values");
+  const uint32_t x = __builtin_bit_cast(uint32_t, a), y = __builtin_bit_cast(uint32_t, b);
+  return __builtin_bit_cast(T, (x & ~m) | (y & m));
+}
+template <int P, typename Fn>
+__device__ __forceinline__ auto pick(uint32_t m1, uint32_t m2, Fn f) {
+  if constexpr (P == 1) {
+    return f(0);
+  } else if constexpr (P == 2) {
+    return blend(m1, f(0), f(1));
+  } else {
+    static_assert(P == 4, "column packing");
+    return blend(m2, blend(m1, f(0), f(1)), blend(m1, f(2), f(3)));
+  }
 }
 
 // Merge S split partials for query heads h0 .. h0+nh-1:
@@ -357,22 +422,32 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   const _Float16* Ksr = F::QUANT ? p.Ks + (PAGED ? 0 : (size_t)b * p.sc_bs) + (size_t)h * p.sc_hs : nullptr;
   const _Float16* Vsr = F::QUANT ? p.Vs + (PAGED ? 0 : (size_t)b * p.sc_bs) + (size_t)h * p.sc_hs : nullptr;
 
-  const int n = lane & 15;  // query head column of P^T and O^T; token row of the K operand
+  const int n = lane & 15;  // column of S^T, P^T and O^T; token row of the K operand
   const int R = lane >> 4;  // lane row: K dword group; scores and V of tokens 4R .. 4R+3
+  // Column packing (cols_reduce): column n carries head hh of tile jl of each
+  // group of P tiles; columns past P * HG carry nothing (scores masked).
+  constexpr int P = (16 / HG < U) ? 16 / HG : U;
+  constexpr int NG = U / P;  // tile groups per pass
+  const bool live = n < P * HG;
+  const int jl = live ? n / HG : P - 1;
+  const int hh = n % HG;
+  const uint32_t m1 = (jl & 1) ? ~0u : 0u, m2 = (jl & 2) ? ~0u : 0u;  // pick() masks
 
-  // Query operand B of the score product: lane l holds head n, elements
+  // Query operand B of the score product: lane l holds head hh, elements
   // kd_index(i, R, 0..7). The descriptor covers only this group's hcnt query
-  // rows; head columns past them read zeros and are never emitted.
+  // rows; head columns past them (and dead columns, sent to row 16) read
+  // zeros and are never emitted.
   h8_t qb[F::NKI];
   {
     const rsrc_t rQ = make_rsrc(p.q + qrow0 * D, (uint32_t)hcnt * D * 2);
+    const uint32_t qrow = live ? (uint32_t)hh : 16u;
 #pragma unroll
-    for (int i = 0; i < F::NKI; ++i) qb[i] = F::qfrag(rQ, (uint32_t)n * D, i, R);
+    for (int i = 0; i < F::NKI; ++i) qb[i] = F::qfrag(rQ, qrow * D, i, R);
   }
 
-  float m_run = -INFINITY, l_run = 0.0f;  // of head n, over the tokens this lane scored
+  float m_run = -INFINITY, l_run = 0.0f;  // of column n, over the tokens this lane scored
   int acc_shift = 0;                      // acc holds the true accumulators times 2^acc_shift
-  f4_t acc[VE];                           // O^T: step c, reg k = head-dim VE (4R + k) + c of head n
+  f4_t acc[VE];                           // O^T: step c, reg k = head-dim VE (4R + k) + c of column n
 #pragma unroll
   for (int c = 0; c < VE; ++c) acc[c] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
@@ -380,7 +455,9 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // as zeros (their scores are masked); offsets are 32-bit from the row block.
   // Paged rows get a descriptor per tile instead (a tile never crosses a
   // page), ending at the tile's last valid token; a tile whose page id is out
-  // of range gets an empty descriptor and its tokens are masked.
+  // of range gets an empty descriptor and its tokens are masked. (Per-tile
+  // descriptors for contiguous rows too would spare the vector address adds
+  // but put scalar work ahead of every pass's first load: measured slower.)
   const uint32_t sts = 2u * (uint32_t)p.sc_ts;  // scale stride in bytes
   const rsrc_t rK = make_rsrc(Kr, PAGED ? 0u : (uint32_t)hi * ts);
   const rsrc_t rV = make_rsrc(Vr, PAGED ? 0u : (uint32_t)hi * ts);
@@ -426,32 +503,82 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // All K loads of the pass are issued, then all V loads, before anything is
   // consumed: straight-line code, so the load counter waits exactly for the
   // data about to be used while the rest is still arriving. The pass scores
-  // its U tiles with the matrix cores (S^T: tokens on M, heads on N), takes
-  // ONE online-softmax step over its 16 U tokens per head, and accumulates
-  // O^T += V^T P^T on the matrix cores: the score result layout (lane: head
-  // n, tokens 4R + k) is exactly operand B of the PV product.
+  // its U tiles with the matrix cores (S^T: tokens on M, columns on N), keeps
+  // in column n the scores of tile jl of each group of P tiles, takes ONE
+  // online-softmax step over the pass, and accumulates O^T += V^T P^T on the
+  // matrix cores: the packed score layout (lane: column n, tokens 4R + k) is
+  // operand B of the PV product of tile jl, zero for the group's other tiles,
+  // so column n of O^T gathers tile jl's share of head hh.
   const int step = 16 * nw;
+  const int lane_tok = jl * step + 4 * R;  // token of the lane's first score in a group, from its base
+  // scales of paged rows come through per-tile descriptors: every tile's are
+  // loaded and the lane's tile is picked afterwards
+  constexpr bool PICK_SC = F::QUANT && PAGED && P > 1;
+  // contiguous, 8-byte aligned scale rows: a lane's four scales (tokens 4R ..
+  // 4R + 3, a multiple of 4 from lo) are one 8-byte load in passes that lie
+  // wholly before hi (a load straddling the descriptor's end could be dropped
+  // whole)
+  const bool vec_sc = F::QUANT && !PAGED && sts == 2u && (lo & 3) == 0 &&
+                      ((reinterpret_cast<uintptr_t>(Ksr) | reinterpret_cast<uintptr_t>(Vsr)) & 7u) == 0;
   for (int pb = lo + 16 * w; pb < hi; pb += U * step) {
     typename F::KT kr[U][F::KL];
     uint32_t vr[U][4][VD];
-    _Float16 ks[U][4], vs[U][4];  // per-token scales of tokens 4R + k (int8 / int4)
+    // per-token scales (int8 / int4) of tokens 4R + k of the lane's tile in group g
+    _Float16 ks[NG][4], vs[NG][4];
+    _Float16 kt[PICK_SC ? U : 1][4], vt[PICK_SC ? U : 1][4];
     TileSrc src[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) src[u] = tile_src(pb + u * step);
+    const bool full = !PAGED && pb + (U - 1) * step + 16 <= hi;  // every token of the pass is before hi
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      F::load_k(src[u].k, src[u].off + koff, kr[u]);
+    for (int u = 0; u < U; ++u) F::load_k(src[u].k, src[u].off + koff, kr[u]);
+    if constexpr (F::QUANT) {
+      if constexpr (!PAGED) {
+        if (vec_sc && full) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        if constexpr (F::QUANT) {
-          const uint32_t so = src[u].soff + (uint32_t)(4 * R + k) * sts;
-          ks[u][k] = __builtin_bit_cast(_Float16, buf_load<2>(src[u].ks, so));
-          vs[u][k] = __builtin_bit_cast(_Float16, buf_load<2>(src[u].vs, so));
+          for (int g = 0; g < NG; ++g) {
+            const uint32_t so = (uint32_t)(pb + g * P * step + lane_tok) * 2u;
+            const u2_t a = buf_load<8>(rKs, so), c = buf_load<8>(rVs, so);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              ks[g][k] = __builtin_bit_cast(_Float16, (uint16_t)(a[k / 2] >> (16 * (k % 2))));
+              vs[g][k] = __builtin_bit_cast(_Float16, (uint16_t)(c[k / 2] >> (16 * (k % 2))));
+            }
+          }
         } else {
-          ks[u][k] = (_Float16)1.0f;
-          vs[u][k] = (_Float16)1.0f;
+#pragma unroll
+          for (int g = 0; g < NG; ++g) {
+            const uint32_t so = (uint32_t)(pb + g * P * step + lane_tok) * sts;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              ks[g][k] = __builtin_bit_cast(_Float16, buf_load<2>(rKs, so + (uint32_t)k * sts));
+              vs[g][k] = __builtin_bit_cast(_Float16, buf_load<2>(rVs, so + (uint32_t)k * sts));
+            }
+          }
         }
+      } else {
+        constexpr int T = PICK_SC ? U : NG;  // P == 1 otherwise: tile g is group g
+#pragma unroll
+        for (int u = 0; u < T; ++u)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t so = src[u].soff + (uint32_t)(4 * R + k) * sts;
+            const _Float16 a = __builtin_bit_cast(_Float16, buf_load<2>(src[u].ks, so));
+            const _Float16 c = __builtin_bit_cast(_Float16, buf_load<2>(src[u].vs, so));
+            if constexpr (PICK_SC) {
+              kt[u][k] = a;
+              vt[u][k] = c;
+            } else {
+              ks[u][k] = a;
+              vs[u][k] = c;
+            }
+          }
       }
+    } else {
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ks[g][k] = vs[g][k] = (_Float16)1.0f;
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -460,6 +587,17 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       for (int j = 0; j < 4; ++j) load_vchunk<VG::VBYTES, VD>(src[u].v, base + (uint32_t)(4 * j) * ts, vr[u][j]);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
+
+    if constexpr (PICK_SC) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          auto bits = [](_Float16 v) { return (uint32_t)__builtin_bit_cast(uint16_t, v); };
+          ks[g][k] = __builtin_bit_cast(_Float16, (uint16_t)pick<P>(m1, m2, [&](int j) { return bits(kt[g * P + j][k]); }));
+          vs[g][k] = __builtin_bit_cast(_Float16, (uint16_t)pick<P>(m1, m2, [&](int j) { return bits(vt[g * P + j][k]); }));
+        }
+    }
 
     f4_t c4[U];
 #pragma unroll
@@ -470,76 +608,140 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
         c4[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(F::kfrag(kr[u], i), qb[i], c4[u], 0, 0, 0);
     }
 
-    float x[U][4];
+    // scores of the lane's tiles; tokens past the split (or on a bad page)
+    // and dead columns are masked
+    float x[NG][4];
+#pragma unroll
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) x[g][k] = pick<P>(m1, m2, [&](int j) { return c4[g * P + j][k]; }) * (float)ks[g][k];
+    if (!full) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          bool ok = pb + g * P * step + lane_tok + k < hi;
+          if constexpr (PAGED) ok = ok && pick<P>(m1, m2, [&](int j) { return src[g * P + j].ok ? ~0u : 0u; }) != 0u;
+          x[g][k] = ok ? x[g][k] : -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int g = 0; g < NG; ++g)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const bool ok = src[u].ok && pb + u * step + 4 * R + k < hi;
-        x[u][k] = ok ? c4[u][k] * (float)ks[u][k] : -INFINITY;
-        mx = fmaxf(mx, x[u][k]);
+        if constexpr (P * HG < 16) x[g][k] = live ? x[g][k] : -INFINITY;
+        mx = fmaxf(mx, x[g][k]);
       }
-    const float mn = fmaxf(m_run, rows4_max(mx));
+    const float mn = fmaxf(m_run, rows4_max(cols_reduce<HG, P, true>(mx)));
     const float mu = (mn == -INFINITY) ? 0.0f : mn;
-    const float alpha = fast_exp2((m_run - mu) * p.c);
+    const float alpha = fast_exp2((m_run - mu) * p.c);  // exactly 1 while the maximum holds
     // The PV operand carries each fp32 weight w = p * (V scale) as an fp16
-    // pair hi + lo (hi = fp16(w'), lo = fp16(w' - hi)): two matrix-core steps
+    // pair hi + lo (hi = w' truncated to fp16, lo = fp16(w' - hi)): two matrix-core steps
     // reproduce the weight to ~2^-22 relative, V being exact in fp16. For
     // int8 / int4, w' = w * 2^shift with a power-of-two shift that puts the
-    // pass's largest possible weight just under 2^14, so lo stays clear of the
-    // fp16 subnormals (small per-token scales would otherwise push it there,
-    // against V values up to 127); acc is then kept in units of 2^shift and
-    // rescaled exactly when the shift changes. fp16 weights (w = p <= 1, V
+    // pass's largest possible weight at most 2^2 under 2^14, so lo stays clear
+    // of the fp16 subnormals (small per-token scales would otherwise push it
+    // there, against V values up to 127). The shift only changes when the
+    // pass's V scales leave that window; l and acc are kept in units of
+    // 2^shift and rescaled exactly when it does. fp16 weights (w = p <= 1, V
     // values of unit size) need no shift.
     int shift = 0;
     if constexpr (F::QUANT) {
       float vmax = 0.0f;
 #pragma unroll
-      for (int u = 0; u < U; ++u)
+      for (int g = 0; g < NG; ++g)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) vmax = fmaxf(vmax, (float)vs[u][k]);
-      vmax = rows4_max(vmax);
+        for (int k = 0; k < 4; ++k) vmax = fmaxf(vmax, (float)vs[g][k]);
+      // over the pass (dead columns hold scales of the pass's last tile)
+      vmax = rows4_max(cols_reduce<HG, P, true>(vmax));
       // vmax < 2^e with e from the exponent field (vmax is a normal fp32)
       const int e = vmax > 0.0f ? (int)((__builtin_bit_cast(uint32_t, vmax) >> 23) & 0xFFu) - 126 : 0;
-      shift = 14 - e;
+      const int ideal = 14 - e;
+      shift = (acc_shift <= ideal && acc_shift >= ideal - 2) ? acc_shift : ideal;
     }
-    h4_t phi[U], plo[U];
+    // p 2^shift = 2^((x - mu) c + shift), the argument as one multiply-add
+    const float arg0 = (float)shift - mu * p.c;
+    h4_t phi[NG], plo[NG];
     float psum = 0.0f;
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int g = 0; g < NG; ++g) {
+      float wv[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const float pw = fast_exp2((x[u][k] - mu) * p.c);
+        const float pw = fast_exp2(fmaf(x[g][k], p.c, arg0));
         psum += pw;
-        const float wv = F::QUANT ? __builtin_amdgcn_ldexpf(pw * (float)vs[u][k], shift) : pw;
-        const _Float16 h = (_Float16)wv;
-        phi[u][k] = h;
-        plo[u][k] = (_Float16)(wv - (float)h);
+        wv[k] = F::QUANT ? pw * (float)vs[g][k] : pw;
       }
-    l_run = l_run * alpha + psum;
-    m_run = mn;
+      // hi through an explicit conversion (round toward zero): converting
+      // with a cast lets the compiler fuse the product into a mixed-precision
+      // multiply-add for one use and not another, and the two roundings of w
+      // to fp16 can differ, leaving hi + lo an fp16 ulp off w
+      const h2_t h01 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(wv[0], wv[1]));
+      const h2_t h23 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(wv[2], wv[3]));
+      const h2_t l01 = __builtin_bit_cast(
+          h2_t, __builtin_amdgcn_cvt_pkrtz(wv[0] - (float)h01.x, wv[1] - (float)h01.y));
+      const h2_t l23 = __builtin_bit_cast(
+          h2_t, __builtin_amdgcn_cvt_pkrtz(wv[2] - (float)h23.x, wv[3] - (float)h23.y));
+      phi[g] = h4_t{h01.x, h01.y, h23.x, h23.y};
+      plo[g] = h4_t{l01.x, l01.y, l23.x, l23.y};
+    }
     const float acc_alpha = F::QUANT ? __builtin_amdgcn_ldexpf(alpha, shift - acc_shift) : alpha;
+    l_run = l_run * acc_alpha + psum;
     acc_shift = shift;
+    // acc needs rescaling only where the maximum or the shift moved and
+    // something has been accumulated (acc is all zero while m = -inf)
+    if (__builtin_amdgcn_ballot_w64(acc_alpha != 1.0f && m_run != -INFINITY) != 0) {
 #pragma unroll
-    for (int c = 0; c < VE; ++c) acc[c] *= acc_alpha;
+      for (int c = 0; c < VE; ++c) acc[c] *= acc_alpha;
+    }
+    m_run = mn;
+    // Two tiles per product: v_mfma_f32_16x16x32_f16 contracts over 32
+    // operand slots, lane row R's slots 8R .. 8R+3 taking tokens 4R .. 4R+3
+    // of tile u and 8R+4 .. 8R+7 the same tokens of tile u + 1 (half the
+    // matrix-core time of two 16x16x16 products).
+    static_assert(U % 2 == 0, "tiles are paired");
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < U; u += 2) {
+      // operand B of tile t: the weights of the columns that hold tile t
+      auto wts = [&](int t, h4_t& bh, h4_t& bl) {
 #pragma unroll
-      for (int dw = 0; dw < VD; ++dw) exchange_4x4(vr[u][0][dw], vr[u][1][dw], vr[u][2][dw], vr[u][3][dw]);
-      h4_t vf[VE];
+        for (int dw = 0; dw < VD; ++dw) exchange_4x4(vr[t][0][dw], vr[t][1][dw], vr[t][2][dw], vr[t][3][dw]);
+        bh = phi[t / P];
+        bl = plo[t / P];
+        if constexpr (P > 1) {
+          const bool mine = jl == t % P;
+          const u2_t h2 = __builtin_bit_cast(u2_t, bh), l2 = __builtin_bit_cast(u2_t, bl);
+          bh = __builtin_bit_cast(h4_t, u2_t{mine ? h2.x : 0u, mine ? h2.y : 0u});
+          bl = __builtin_bit_cast(h4_t, u2_t{mine ? l2.x : 0u, mine ? l2.y : 0u});
+        }
+      };
+      h4_t bh0, bl0, bh1, bl1;
+      wts(u, bh0, bl0);
+      wts(u + 1, bh1, bl1);
+      const h8_t bh = __builtin_shufflevector(bh0, bh1, 0, 1, 2, 3, 4, 5, 6, 7);
+      const h8_t bl = __builtin_shufflevector(bl0, bl1, 0, 1, 2, 3, 4, 5, 6, 7);
+      h8_t vf[VE];
 #pragma unroll
       for (int c = 0; c < VE; ++c) {
-        vf[c] = vfrag<FMT, D>(vr[u], c);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[c], phi[u], acc[c], 0, 0, 0);
+        vf[c] = __builtin_shufflevector(vfrag<FMT, D>(vr[u], c), vfrag<FMT, D>(vr[u + 1], c), 0, 1, 2, 3, 4, 5, 6, 7);
+        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[c], bh, acc[c], 0, 0, 0);
       }
 #pragma unroll
-      for (int c = 0; c < VE; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x16f16(vf[c], plo[u], acc[c], 0, 0, 0);
+      for (int c = 0; c < VE; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[c], bl, acc[c], 0, 0, 0);
     }
   }
 
-  // ---- wave totals: l over the four lane rows; O^T rows are disjoint ----
-  l_run = rows4_sum(l_run);
+  // ---- wave totals: l over the four lane rows; O^T rows are disjoint; the
+  // P columns of a head add up (same running max and shift in all of them) ----
+  if constexpr (F::QUANT) l_run = __builtin_amdgcn_ldexpf(l_run, -acc_shift);
+  l_run = cols_reduce<HG, P, false>(rows4_sum(l_run));
+  if constexpr (P > 1) {
+#pragma unroll
+    for (int c = 0; c < VE; ++c)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[c][k] = cols_reduce<HG, P, false>(acc[c][k]);
+  }
   if constexpr (F::QUANT) {
 #pragma unroll
     for (int c = 0; c < VE; ++c)
@@ -581,7 +783,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-      int* ctr = &g_split_arrivals[p.slot][wsg];
+      int* ctr = arrival_counter(p.slot, wsg);
       s_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.S - 1;
     }
     __syncthreads();
@@ -589,7 +791,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       merge_splits<D, CPOL_SC1>(p.m_part, p.l_part, p.o_part, p.o, qrow0, hcnt, p.S, s_mw, s_mr);
       // every workgroup of the group has counted in: reset for the next call
       if (threadIdx.x == 0)
-        __hip_atomic_store(&g_split_arrivals[p.slot][wsg], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(arrival_counter(p.slot, wsg), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }

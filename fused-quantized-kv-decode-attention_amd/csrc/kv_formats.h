@@ -21,7 +21,8 @@
 //
 // Exactness: int8 and int4 values become fp16 through the 0x6400 exponent
 // trick (1024 + u is exact in fp16 for 0 <= u < 1024) followed by an exact
-// subtraction, so the dequantised value (float)q * (float)scale
+// subtraction (or, for int4 high nibbles held as 1024 + 16 u, an exact fused
+// multiply-add), so the dequantised value (float)q * (float)scale
 // (decode_attn_int8_mw.cu:24,31; decode_attn_int4.cu:21-23,29-31) is
 // reproduced bit for bit by fqkv_dequant_kv, which calls these same helpers.
 #pragma once
@@ -59,17 +60,30 @@ __device__ __forceinline__ void i8x4_to_h2x2(uint32_t w, h2_t& a, h2_t& b) {
   b = bytes_under_1024(t, SEL_B23) - off;
 }
 
-// Eight int4 (one dword, byte k = elements 2k (low nibble) and 2k+1) -> four
-// exact half2 in the order [e0 e2 | e4 e6 | e1 e3 | e5 e7].
-__device__ __forceinline__ void i4x8_to_h2x4(uint32_t w, h2_t (&h)[4]) {
-  const uint32_t t = w ^ 0x88888888u;  // nibble n -> n + 8 (mod 16) in [0, 15]
-  const uint32_t lo = t & 0x0F0F0F0Fu;
-  const uint32_t hi = (t >> 4) & 0x0F0F0F0Fu;
+// Two int4 of a dword -> exact half2, one bitwise op and one packed fp16 op
+// each. The nibbles at bits 0-3 and 16-19 (nib_lo) or 4-7 and 20-23
+// (nib_hi) are masked out and placed, sign bit flipped (n ^ 8 = n + 8 mod
+// 16), under the 0x64 exponent byte: 1024 + (n ^ 8), or 1024 + 16 (n ^ 8)
+// for the high nibbles; x - 1032 and x / 16 - 72 (one fused multiply-add,
+// every intermediate exact) then give n.
+__device__ __forceinline__ h2_t nib_lo(uint32_t t) {
   const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
-  h[0] = bytes_under_1024(lo, SEL_B01) - off;
-  h[1] = bytes_under_1024(lo, SEL_B23) - off;
-  h[2] = bytes_under_1024(hi, SEL_B01) - off;
-  h[3] = bytes_under_1024(hi, SEL_B23) - off;
+  return __builtin_bit_cast(h2_t, (t & 0x000F000Fu) ^ 0x64086408u) - off;
+}
+__device__ __forceinline__ h2_t nib_hi(uint32_t t) {
+  const h2_t sc = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const h2_t off = {(_Float16)-72.0f, (_Float16)-72.0f};
+  return __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (t & 0x00F000F0u) ^ 0x64806480u), sc, off);
+}
+
+// Eight int4 (one dword, byte k = elements 2k (low nibble) and 2k+1) -> four
+// exact half2 in the order [e0 e4 | e1 e5 | e2 e6 | e3 e7].
+__device__ __forceinline__ void i4x8_to_h2x4(uint32_t w, h2_t (&h)[4]) {
+  const uint32_t w2 = w >> 8;
+  h[0] = nib_lo(w);
+  h[1] = nib_hi(w);
+  h[2] = nib_lo(w2);
+  h[3] = nib_hi(w2);
 }
 
 // Raw buffer access (gfx9 descriptor word 3 = 0x00020000, stride 0):
@@ -211,25 +225,22 @@ struct Fmt<KV_I4, D> {
     i4x8_to_h2x4(kr[0][i], h);
     return h8_t{h[0].x, h[0].y, h[1].x, h[1].y, h[2].x, h[2].y, h[3].x, h[3].y};
   }
-  // slot e of step i holds element 8 i + {0,2,4,6,1,3,5,7}[e] of the lane's run
+  // slot e of step i holds element 8 i + {0,4,1,5,2,6,3,7}[e] of the lane's run
   __host__ __device__ static constexpr int kd_index(int i, int kb, int e) {
-    return (D / 4) * kb + 8 * i + (e < 4 ? 2 * e : 2 * (e - 4) + 1);
+    return (D / 4) * kb + 8 * i + e / 2 + 4 * (e % 2);
   }
   __device__ static h8_t qfrag(rsrc_t rq, uint32_t row_elem, int i, int kb) {
     const h8_t v = __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
-    return h8_t{v[0], v[2], v[4], v[6], v[1], v[3], v[5], v[7]};
+    return h8_t{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
   }
   // nibble pos (element pos; byte pos / 2, low nibble first) of dwords a and
-  // b -> exact half2 (a_pos, b_pos): n ^ 8 = n + 8 (mod 16) under the 0x64
-  // exponent byte (1024 + n + 8), then 1032 is subtracted.
+  // b -> exact half2 (a_pos, b_pos): byte pos / 2 of a and of b go to bytes
+  // 0 and 2, whose low or high nibbles nib_lo / nib_hi convert.
   __device__ static h2_t vpair(uint32_t a, uint32_t b, int pos) {
     const uint32_t byte = (uint32_t)(pos >> 1);
     const uint32_t sel = 0x0C000C00u | ((4u + byte) << 16) | byte;
-    uint32_t t = __builtin_amdgcn_perm(b, a, sel);
-    if (pos & 1) t >>= 4;
-    t = (t & 0x000F000Fu) ^ 0x64086408u;
-    const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
-    return __builtin_bit_cast(h2_t, t) - off;
+    const uint32_t t = __builtin_amdgcn_perm(b, a, sel);
+    return (pos & 1) ? nib_hi(t) : nib_lo(t);
   }
 };
 
