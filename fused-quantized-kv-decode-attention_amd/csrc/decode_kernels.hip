@@ -14,18 +14,19 @@
 //      64 contiguous bytes of 16 rows per dwordx4 instruction) and the V tile
 //      as four loads of 4 whole rows each,
 //   2. computes the transposed scores S^T = K Q^T (tokens on M, query heads
-//      on N) with D/32 v_mfma_f32_16x16x32_f16, so lane l holds head l % 16
-//      for tokens 4 (l / 16) .. + 3,
+//      on N) with D/32 v_mfma_f32_16x16x32_f16; column n carries head
+//      n % HG, and lane l keeps the scores of tile (l % 16) / HG of each
+//      group of 16 / HG tiles (column packing), tokens 4 (l / 16) .. + 3,
 //   3. runs one online-softmax step per pass with v_exp_f32 (exp(x) =
 //      2^(x log2 e), log2 e folded into the score scale) and an all-reduce
-//      over the four lane rows; the weights p (times the per-token V scale
-//      for int8/int4), as fp16 pairs hi + lo, are then already in operand-B
-//      layout of
-//   4. O^T += V^T P^T with D/16 v_mfma_f32_16x16x16_f16, after a 4 x 4
-//      exchange of the V chunks between lane rows and registers
-//      (v_permlane32_swap / v_permlane16_swap) puts four tokens of one
-//      head-dim element in each operand slot; int8/int4 become exact fp16 on
-//      the way.
+//      over the head's columns and the four lane rows; the weights p (times
+//      the per-token V scale for int8/int4), as fp16 pairs hi + lo, are then
+//      already in operand-B layout of
+//   4. O^T += V^T P^T with D/16 v_mfma_f32_16x16x32_f16 per pair of tiles,
+//      after a 4 x 4 exchange of the V chunks between lane rows and
+//      registers (v_permlane32_swap / v_permlane16_swap) puts four tokens of
+//      one head-dim element in each operand slot; int8/int4 become exact
+//      fp16 on the way.
 // Waves of a workgroup take interleaved tiles; their (m, l, acc) states are
 // merged through LDS. With one split the workgroup writes the normalised
 // fp16 output; otherwise it writes the reference's fp32 scratch layout
