@@ -110,6 +110,23 @@ def test_paged(fmt, page, hnd):
         assert maxerr(out[b], ref) <= TOL, (b, lens[b])
 
 
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("Hq,Hkv", [(8, 8), (40, 5)])
+def test_paged_quant_group_widths(fmt, Hq, Hkv):
+    """Paged int8/int4 caches at one query head per KV head (four tiles share the
+    score columns) and at G = 5 (head group of 8, two tiles share them): the
+    per-tile scale descriptors are picked per lane."""
+    g = torch.Generator().manual_seed(54)
+    lens = [5, 16, 33, 700]
+    D = 128
+    Kp, Vp, Ks, Vs, table, sl, seqs = paged_cache(g, lens, Hkv, D, 32, fmt)
+    q = draw(g, len(lens), Hq, D).half()
+    out = fq.decode_attn_gqa_paged(q.cuda(), Kp, Vp, table, sl, max(lens), 4, Ks, Vs)
+    for b, (Kb, Vb) in enumerate(seqs):
+        ref = oracle.gqa_attention(q.numpy()[b:b + 1], Kb[None], Vb[None])[0]
+        assert maxerr(out[b], ref) <= TOL, (b, lens[b])
+
+
 def test_paged_d64_long_and_split():
     """One long sequence (internal split over many pages) and D = 64."""
     g = torch.Generator().manual_seed(53)

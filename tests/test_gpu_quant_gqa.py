@@ -50,8 +50,26 @@ def test_gqa_quantized(fmt, B, Hq, Hkv, N, D, W):
 
 
 @pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("Hq,Hkv", [(32, 32), (32, 16), (24, 8), (40, 5), (7, 1), (48, 3)])
+def test_gqa_quantized_group_sizes(fmt, D, Hq, Hkv):
+    """Every head-group width of the kernel over quantized caches: groups of 1, 2
+    and 4 heads (four tiles share the 16 score columns), 8 (two tiles) and 16
+    (one), full and partial (G = 3, 5, 7 leave columns without a head)."""
+    B, N = 2, 333
+    g = torch.Generator().manual_seed(43)
+    q = draw(g, B, Hq, D).half()
+    Kq, Ks, Kf = quantized(fmt, draw(g, B, Hkv, N, D))
+    Vq, Vs, Vf = quantized(fmt, draw(g, B, Hkv, N, D))
+    f = fq.decode_attn_gqa_int8 if fmt == "int8" else fq.decode_attn_gqa_int4
+    out = f(q.cuda(), Kq, Vq, Ks, Vs, 4)
+    assert maxerr(out, oracle.gqa_attention(q.numpy(), Kf, Vf)) <= TOL
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
 @pytest.mark.parametrize("Hq,Hkv,N,D,S,W", [(32, 8, 16384, 128, 32, 8), (8, 2, 100, 64, 7, 4),
-                                            (4, 4, 3, 128, 8, 8), (64, 4, 5000, 128, 16, 8)])
+                                            (4, 4, 3, 128, 8, 8), (64, 4, 5000, 128, 16, 8),
+                                            (16, 8, 2000, 128, 16, 8), (40, 5, 1500, 64, 12, 4)])
 def test_gqa_sk_fast_quantized(fmt, Hq, Hkv, N, D, S, W, merge_mode):
     g = torch.Generator().manual_seed(41)
     q = draw(g, Hq, D).half()
