@@ -10,9 +10,10 @@
 //     all of them) as long as the query fragment (operand B) uses the same
 //     map, kd_index(). Each format picks the map that keeps its global loads
 //     wide and its int -> fp16 conversion cheap.
-//   * V side: operand A of v_mfma_f32_16x16x16_f16 (O^T += V^T P^T). Lane
-//     (R = l / 16, i = l % 16) loads VBYTES = ROWB / 16 contiguous bytes at
-//     byte VBYTES * i of tile row 4 j + R (j = 0..3: four loads per tile,
+//   * V side: operand A of the P.V product (O^T += V^T P^T; the kernel puts
+//     two tiles in one v_mfma_f32_16x16x32_f16, four operand slots each).
+//     Lane (R = l / 16, i = l % 16) loads VBYTES = ROWB / 16 contiguous bytes
+//     at byte VBYTES * i of tile row 4 j + R (j = 0..3: four loads per tile,
 //     each covering 4 whole rows). A 4 x 4 exchange of those chunks between
 //     lane rows and loads (v_permlane32_swap, v_permlane16_swap) leaves lane
 //     (R, i) with tokens 4 R .. 4 R + 3 of head-dim elements VE * i .. + VE-1,
