@@ -23,8 +23,9 @@
  *
  * W (and CW) count 64-lane waves per workgroup. W is a maximum: a split too
  * short to give every wave a full pass of 4 16-token tiles runs on fewer
- * waves (at least 2). Results do not depend on W, CW or S beyond fp32
- * rounding of the merge order.
+ * waves (at least 2), and the single-block entry points use at most 4 waves
+ * once they launch 4 or more workgroups per CU. Results do not depend on W,
+ * CW or S beyond fp32 rounding of the merge order.
  *
  * Return value: FQKV_OK (0) on success; otherwise a non-zero FQKV_ERR_* code
  * and fqkv_last_error() describes the failure (thread-local). Argument
