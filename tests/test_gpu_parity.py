@@ -112,6 +112,36 @@ def test_int4_notebook_gate(B, N, W, D):
     assert maxerr(out, ref) <= TOL
 
 
+@pytest.mark.parametrize("fmt", ["fp16", "int8", "int4"])
+@pytest.mark.parametrize("D", [64, 128])
+def test_mha_large_grid_four_wave_workgroups(fmt, D):
+    """Over 4 workgroups per CU the entry points run 4-wave workgroups whatever W
+    asks; the result must not change: oracle parity, and W = 8 equals W = 4 bit for
+    bit (same workgroup shape)."""
+    B, N = 1200, 40
+    g = torch.Generator().manual_seed(9)
+    q = draw(g, B, D).half()
+    Kx, Vx = draw(g, B, N, D), draw(g, B, N, D)
+    if fmt == "fp16":
+        K, V = Kx.half(), Vx.half()
+        run = lambda W: fq.decode_attn_fp16_mw(gpu(q), gpu(K), gpu(V), W)
+        Kf, Vf = K.float().numpy(), V.float().numpy()
+    elif fmt == "int8":
+        K, Ks = quant.quant_int8_per_token(Kx)
+        V, Vs = quant.quant_int8_per_token(Vx)
+        run = lambda W: fq.decode_attn_int8_mw(gpu(q), gpu(K), gpu(V), gpu(Ks), gpu(Vs), W)
+        Kf, Vf = oracle.dequant_int8(K.numpy(), Ks.numpy()), oracle.dequant_int8(V.numpy(), Vs.numpy())
+    else:
+        K, Ks = quant.quant_int4_per_token(Kx)
+        V, Vs = quant.quant_int4_per_token(Vx)
+        run = lambda W: fq.decode_attn_int4(gpu(q), gpu(K), gpu(V), gpu(Ks), gpu(Vs), W)
+        Kf, Vf = oracle.dequant_int4(K.numpy(), Ks.numpy()), oracle.dequant_int4(V.numpy(), Vs.numpy())
+    out8, out4 = run(8), run(4)
+    assert maxerr(out8, oracle.attention(q.numpy(), Kf, Vf)) <= TOL
+    if B >= 4 * torch.cuda.get_device_properties(0).multi_processor_count:
+        assert torch.equal(out8, out4)
+
+
 def test_int4_all_bytes():
     B, N, D = 3, 777, 128
     g = torch.Generator().manual_seed(4)
