@@ -400,9 +400,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // wave index as a scalar, so tile loops branch per wave, not per lane
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
-  // blockIdx.x = (r * ngroups + hg) * S + s, decomposed with multiply-shift divisions
-  const uint32_t wsg = fast_div(blockIdx.x, p.div_S);
-  const int s = (int)(blockIdx.x - wsg * (uint32_t)p.S);
+  // blockIdx.x = s * nwsg + wsg or wsg * S + s (wsg = r * ngroups + hg),
+  // decomposed with multiply-shift divisions
+  const uint32_t bq = fast_div(blockIdx.x, p.div_blk);
+  const uint32_t br = blockIdx.x - bq * (uint32_t)p.blk_d;
+  const uint32_t wsg = p.split_major ? br : bq;
+  const int s = (int)(p.split_major ? bq : br);
   const uint32_t rr = fast_div(wsg, p.div_groups);
   const int hg = (int)(wsg - rr * (uint32_t)p.ngroups);
   const int r = (int)rr;
@@ -869,7 +872,8 @@ static hipError_t launch_partial_d(int hg, const PartialParams& p, int nblocks, 
 
 hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, int nblocks, int nw,
                           hipStream_t st) {
-  if ((nw != 2 && nw != 4 && nw != 8) || nblocks < 1 || params.S < 1 || params.ngroups < 1 || params.hkv < 1)
+  if ((nw != 2 && nw != 4 && nw != 8) || nblocks < 1 || params.S < 1 || params.ngroups < 1 || params.hkv < 1 ||
+      nblocks % params.S != 0)
     return hipErrorInvalidValue;
   // nw is a maximum: a split shorter than one pass of nw waves would leave
   // waves with nothing to load, so take the fewest waves (at least 2) that
@@ -880,7 +884,9 @@ hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, i
   const int units = params.S > 1 ? hg * (D / 64) : 1;
   while (nw > 2 && nw / 2 >= units && (nw / 2) * TILES_PER_PASS >= tiles) nw /= 2;
   PartialParams p = params;
-  p.div_S = make_fastdiv((uint32_t)p.S);
+  p.split_major = p.S >= 16;
+  p.blk_d = p.split_major ? nblocks / p.S : p.S;
+  p.div_blk = make_fastdiv((uint32_t)p.blk_d);
   p.div_groups = make_fastdiv((uint32_t)p.ngroups);
   p.div_hkv = make_fastdiv((uint32_t)p.hkv);
   switch (fmt) {
