@@ -206,7 +206,9 @@ __device__ __forceinline__ auto pick(uint32_t m1, uint32_t m2, Fn f) {
 // chunk, so a merge costs about one memory round trip (two when S > 64).
 // When there are fewer units than waves, the splits of a unit are cut into
 // nsl slices on different waves and the slices meet in LDS (the only
-// barrier; its condition is the same for the whole workgroup).
+// barrier; its condition is the same for the whole workgroup). With at most
+// CHK splits and no more units than waves everything is one chunk per wave,
+// and a short path skips the slice bookkeeping.
 // CPOL: cache policy of the partial loads (CPOL_SC1 for partials that other
 // workgroups of the same launch stored at device scope).
 // s_w: 64 floats per wave (16-byte aligned rows); s_red: 65 floats per wave.
@@ -220,12 +222,6 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
   const int units = nh * DB;
-  // nsl = 2^lg slices per unit; waves wv with equal wv >> lg share a unit
-  int lg = 0;
-  while ((2 << lg) * units <= nw && (2 << lg) * CHK <= S) ++lg;
-  const int nsl = 1 << lg;
-  const int cu = nw >> lg;                                              // units per round
-  const int len = (((S + nsl - 1) >> lg) + CHK - 1) & ~(CHK - 1);      // splits per slice
   auto ld = [](rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, CPOL));
   };
@@ -233,6 +229,47 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
   auto ldo = [](rsrc_t r, uint32_t lane_off, uint32_t row_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)lane_off, (int)row_off, CPOL));
   };
+  if (S <= CHK && units <= nw) {
+    // One chunk per unit and a wave per unit (the batch-1 split-K case):
+    // wave wv merges unit wv with no slice bookkeeping, so its loads leave
+    // a few scalar instructions after the merge is known to be needed.
+    if (wv < units) {
+      const int h = wv / DB;
+      const size_t hrow = h0 + h;
+      const rsrc_t rM = make_rsrc(m_part + hrow * S, (uint32_t)S * 4u);
+      const rsrc_t rL = make_rsrc(l_part + hrow * S, (uint32_t)S * 4u);
+      const rsrc_t rO = make_rsrc(o_part + hrow * S * D + (wv - h * DB) * 64, (uint32_t)(S - 1) * D * 4u + 256u);
+      const uint32_t lo4 = (uint32_t)lane * 4u;
+      const float m0 = ld(rM, lo4);
+      const float l0 = ld(rL, lo4);
+      float ov[CHK];
+#pragma unroll
+      for (int k = 0; k < CHK; ++k) ov[k] = ldo(rO, lo4, (uint32_t)(k * D * 4));  // zero past split S - 1
+      float M = wave_max(lane < S ? m0 : -INFINITY);
+      if (M == -INFINITY) M = 0.0f;  // every split empty: all weights 0
+      const float w = lane < S ? fast_exp2((m0 - M) * LOG2E) : 0.0f;
+      s_w[wv][lane] = w;
+      const float L = wave_sum(w * l0);
+      const fl4_t* w4 = reinterpret_cast<const fl4_t*>(&s_w[wv][0]);
+      fl4_t acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int k = 0; k < CHK / 4; ++k) {
+        const fl4_t wk = w4[k];
+        acc4.x = fmaf(wk.x, ov[4 * k], acc4.x);
+        acc4.y = fmaf(wk.y, ov[4 * k + 1], acc4.y);
+        acc4.z = fmaf(wk.z, ov[4 * k + 2], acc4.z);
+        acc4.w = fmaf(wk.w, ov[4 * k + 3], acc4.w);
+      }
+      o[hrow * D + (wv - h * DB) * 64 + lane] = (_Float16)(((acc4.x + acc4.y) + (acc4.z + acc4.w)) / L);
+    }
+    return;
+  }
+  // nsl = 2^lg slices per unit; waves wv with equal wv >> lg share a unit
+  int lg = 0;
+  while ((2 << lg) * units <= nw && (2 << lg) * CHK <= S) ++lg;
+  const int nsl = 1 << lg;
+  const int cu = nw >> lg;                                              // units per round
+  const int len = (((S + nsl - 1) >> lg) + CHK - 1) & ~(CHK - 1);      // splits per slice
   for (int ub = 0; ub < units; ub += cu) {  // a single round when nsl > 1
     const int u = ub + (wv >> lg);
     const int sl = wv & (nsl - 1);
