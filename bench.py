@@ -3,9 +3,10 @@
 Workload (the headline metric's configuration): ``gqa_sk_fast`` with 32 query
 heads / 8 KV heads, N = 16384 cached tokens, head_dim 128, batch 1, fp16
 q/K/V drawn N(0,1), fp32 split scratch preallocated. One step = one call of
-the entry point (partial kernel + combine kernel) on the next of ``--kv-sets``
+the entry point on the next of ``--kv-sets``
 distinct KV caches, so successive steps stream >= 512 MiB of distinct KV and
-the 256 MB Infinity Cache cannot serve them. Inputs are resident in HBM
+the 256 MB Infinity Cache cannot serve them. A call is one kernel launch:
+the partial kernel with the split merge fused in. Inputs are resident in HBM
 before timing starts.
 
 Reported: ``value`` = algorithmic bytes per call / time per call in GB/s
@@ -458,6 +459,85 @@ def suite_splitk_quant(torch, fq, steps, warmup, rows):
             torch.cuda.empty_cache()
 
 
+def suite_paged(torch, fq, steps, warmup, rows):
+    """decode_attn_gqa_paged (Hq 32, Hkv 8, D 128, B 8, N 32768) over NHD pages of 16 / 64 / 256
+    tokens and head-major (HND) pages of 64 tokens at shuffled page ids, fp16 / int8 / int4, next
+    to the contiguous decode_attn_gqa[_int8|_int4] over the same tokens: what the page indirection
+    costs at a 1 GB cache."""
+    B, Hq, Hkv, N, Dd, W = 8, 32, 8, 32768, 128, 8
+    G = Hq // Hkv
+    g = torch.Generator(device="cuda").manual_seed(11)
+    q = torch.randn(B, Hq, Dd, device="cuda", generator=g).half()
+    sl = torch.full((B,), N, dtype=torch.int32, device="cuda")
+    nsteps, nwarm = max(50, steps // 4), max(10, warmup // 4)
+    for fmt in ("fp16", "int8", "int4"):
+        Xk = torch.randn(B * Hkv, N, Dd, device="cuda", generator=g)
+        Xv = torch.randn(B * Hkv, N, Dd, device="cuda", generator=g)
+        if fmt == "fp16":
+            K, V, Ks, Vs = Xk.half(), Xv.half(), None, None
+            Kf, Vf = K[:Hkv].float(), V[:Hkv].float()
+            contiguous = lambda: fq.decode_attn_gqa(q, K.view(B, Hkv, N, Dd), V.view(B, Hkv, N, Dd), W)
+            kvb = 4 * Hkv * N * Dd
+        else:
+            quantize = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+            (K, Ks), (V, Vs) = quantize(Xk), quantize(Xv)
+            if fmt == "int8":
+                Kf, Vf = K[:Hkv].float() * Ks[:Hkv].float()[..., None], V[:Hkv].float() * Vs[:Hkv].float()[..., None]
+            else:
+                from fqkv_decode import quant
+                Kf, Vf = quant.dequant_int4(K[:Hkv], Ks[:Hkv]), quant.dequant_int4(V[:Hkv], Vs[:Hkv])
+            f = fq.decode_attn_gqa_int8 if fmt == "int8" else fq.decode_attn_gqa_int4
+            rb = K.shape[-1]
+            contiguous = lambda: f(q, K.view(B, Hkv, N, rb), V.view(B, Hkv, N, rb), Ks.view(B, Hkv, N),
+                                   Vs.view(B, Hkv, N), W)
+            kvb = 2 * Hkv * N * rb + 4 * Hkv * N
+        del Xk, Xv
+        # sequence 0 against float32 attention over its (dequantized) cache
+        ref0 = _ref_mha(torch, q[0], Kf.repeat_interleave(G, 0), Vf.repeat_interleave(G, 0))
+        del Kf, Vf
+        nbytes = B * (kvb + 4 * Hq * Dd)
+        o = contiguous()
+        err = float((o[0].float() - ref0).abs().max())
+        ms = _loop_ms(torch, lambda i: contiguous(), 1, nsteps, nwarm)
+        cfg = {"B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": Dd, "W": W, "fmt": fmt}
+        rows.append(_row("gqa_contiguous_" + fmt, cfg, ms, nbytes, err))
+        log("paged suite: contiguous %s        %8.2f us  %7.1f GB/s  err %.2e" % (fmt, ms * 1e3, nbytes / ms / 1e6, err))
+        for page, hnd in ((16, False), (64, False), (256, False), (64, True)):
+            npb = N // page
+            P = B * npb
+            perm = torch.randperm(P, device="cuda", generator=g)
+            table = perm.view(B, npb).to(torch.int32)
+
+            def pages(X):  # [B*Hkv, N, ...] -> [P, page, Hkv, ...] at page ids perm
+                tail = X.shape[2:]
+                if hnd:  # head-major pages [P, Hkv, page, ...], handed over as the NHD view
+                    Y = X.view(B, Hkv, npb, page, *tail).movedim(1, 2).reshape(P, Hkv, page, *tail)
+                    out = torch.empty_like(Y)
+                    out[perm] = Y
+                    return out.transpose(1, 2)
+                Y = X.view(B, Hkv, npb, page, *tail).movedim(1, 3).reshape(P, page, Hkv, *tail)
+                out = torch.empty_like(Y)
+                out[perm] = Y
+                return out
+
+            Kp, Vp = pages(K), pages(V)
+            Ksp, Vsp = (pages(Ks), pages(Vs)) if Ks is not None else (None, None)
+            fn = lambda i: fq.decode_attn_gqa_paged(q, Kp, Vp, table, sl, N, W, Ksp, Vsp)
+            op = fn(0)
+            perr = float((op[0].float() - ref0).abs().max())
+            same = bool(torch.equal(op, o))
+            pb = nbytes + B * npb * 4
+            ms = _loop_ms(torch, fn, 1, nsteps, nwarm)
+            lay = "HND" if hnd else "NHD"
+            rows.append(_row("gqa_paged_" + fmt, dict(cfg, page=page, pages=lay), ms, pb, perr,
+                             equal_to_contiguous=same))
+            log("paged suite: page %-4d %s %s   %8.2f us  %7.1f GB/s  err %.2e  equal to contiguous: %s"
+                % (page, lay, fmt, ms * 1e3, pb / ms / 1e6, perr, same))
+            del Kp, Vp, Ksp, Vsp
+        del K, V, Ks, Vs
+        torch.cuda.empty_cache()
+
+
 def suite_llama(torch, fq, rows):
     """End-to-end decode on a random-init Llama-3.2-1B-shaped model (16 layers, 32/8 heads,
     head_dim 64, hidden 2048, fp16) through transformers, SDPA vs the kernel hook
@@ -547,7 +627,7 @@ def suite_llama(torch, fq, rows):
     torch.cuda.empty_cache()
 
 
-SUITES = ("mha_small", "mha_quant", "gqa", "splitk", "splitk_quant", "llama")
+SUITES = ("mha_small", "mha_quant", "gqa", "splitk", "splitk_quant", "paged", "llama")
 
 
 def run_suite(torch, fq, path, steps=400, warmup=40, only=SUITES):
@@ -562,6 +642,8 @@ def run_suite(torch, fq, path, steps=400, warmup=40, only=SUITES):
         suite_splitk(torch, fq, steps, warmup, rows)
     if "splitk_quant" in only:
         suite_splitk_quant(torch, fq, steps, warmup, rows)
+    if "paged" in only:
+        suite_paged(torch, fq, steps, warmup, rows)
     if "llama" in only:
         suite_llama(torch, fq, rows)
     with open(path, "w") as f:
