@@ -538,6 +538,36 @@ def suite_paged(torch, fq, steps, warmup, rows):
         torch.cuda.empty_cache()
 
 
+def suite_quant(torch, fq, steps, warmup, rows):
+    """quantize_int8_per_token / quantize_int4_per_token on [64, 32768, 128] rows (a B 8, Hkv 8,
+    N 32768 cache side) from fp16 and fp32 inputs; bytes gated equal to the PyTorch expressions
+    of fqkv_decode.quant on the same GPU tensor."""
+    from fqkv_decode import quant
+    rows_, N_, Dd = 64, 32768, 128
+    g = torch.Generator(device="cuda").manual_seed(13)
+    X32 = torch.randn(rows_, N_, Dd, device="cuda", generator=g)
+    for src in ("fp16", "fp32"):
+        X = X32.half() if src == "fp16" else X32
+        for fmt in ("int8", "int4"):
+            f = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+            ref = quant.quant_int8_per_token if fmt == "int8" else quant.quant_int4_per_token
+            q, s = f(X)
+            rq, rs = ref(X[:4])
+            same = bool(torch.equal(q[:4], rq) and torch.equal(s[:4], rs))
+            if not same:
+                log("quantizer %s from %s: bytes differ from the PyTorch expressions" % (fmt, src))
+                continue
+            elems = rows_ * N_ * Dd
+            nbytes = elems * X.element_size() + (elems if fmt == "int8" else elems // 2) + 2 * rows_ * N_
+            ms = _loop_ms(torch, lambda i: f(X), 1, max(50, steps // 4), max(10, warmup // 4))
+            rows.append(_row("quantize_" + fmt, {"rows": rows_ * N_, "D": Dd, "src": src}, ms, nbytes,
+                             equal_to_torch_expressions=same))
+            log("quantizer %s from %s: %8.2f us  %7.1f GB/s" % (fmt, src, ms * 1e3, nbytes / ms / 1e6))
+        del X
+    del X32
+    torch.cuda.empty_cache()
+
+
 def suite_llama(torch, fq, rows):
     """End-to-end decode on a random-init Llama-3.2-1B-shaped model (16 layers, 32/8 heads,
     head_dim 64, hidden 2048, fp16) through transformers, SDPA vs the kernel hook
@@ -627,7 +657,7 @@ def suite_llama(torch, fq, rows):
     torch.cuda.empty_cache()
 
 
-SUITES = ("mha_small", "mha_quant", "gqa", "splitk", "splitk_quant", "paged", "llama")
+SUITES = ("mha_small", "mha_quant", "gqa", "splitk", "splitk_quant", "paged", "quant", "llama")
 
 
 def run_suite(torch, fq, path, steps=400, warmup=40, only=SUITES):
@@ -644,6 +674,8 @@ def run_suite(torch, fq, path, steps=400, warmup=40, only=SUITES):
         suite_splitk_quant(torch, fq, steps, warmup, rows)
     if "paged" in only:
         suite_paged(torch, fq, steps, warmup, rows)
+    if "quant" in only:
+        suite_quant(torch, fq, steps, warmup, rows)
     if "llama" in only:
         suite_llama(torch, fq, rows)
     with open(path, "w") as f:
