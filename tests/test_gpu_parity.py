@@ -279,6 +279,23 @@ def test_gqa_sk_fast_one_head_per_kv_row(D, S, W, merge_mode):
     assert maxerr(o, oracle.combine_partials(m, l, acc)) <= TOL
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("S,W", [(31, 8), (32, 8), (33, 8), (32, 4)])
+def test_gqa_sk_fast_merge_chunk_boundary(D, S, W, merge_mode):
+    """The split merge takes a one-chunk path up to 32 splits when every
+    (head, 64-dim block) has a wave of its own (S 31, 32 at W 8) and the
+    general path past it (S 33) or with fewer waves than blocks (D 128, W 4):
+    all agree with the oracle and with the merge of the oracle's partials."""
+    Hq, Hkv, N = 32, 8, 3000
+    g = torch.Generator().manual_seed(16)
+    q, K, V = draw(g, Hq, D).half(), draw(g, Hkv, N, D).half(), draw(g, Hkv, N, D).half()
+    o, mp, lp, op = run_sk(q, K, V, S, W, 8)
+    ref = oracle.gqa_attention(q.numpy()[None], K.numpy()[None], V.numpy()[None])[0]
+    assert maxerr(o, ref) <= TOL
+    m, l, acc = oracle.split_partials(q.numpy(), K.numpy(), V.numpy(), S)
+    assert maxerr(o, oracle.combine_partials(m, l, acc)) <= TOL
+
+
 def test_gqa_sk_fast_batch_folds_into_heads(merge_mode):
     """Batch B as q [B*Hq, D], K [B*Hkv, N, D]: head b*Hq+j reads KV row b*Hkv + j/G."""
     B, Hq, Hkv, N, D = 3, 32, 8, 2048, 128
