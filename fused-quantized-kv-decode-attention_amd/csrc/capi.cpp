@@ -12,6 +12,9 @@
 #include <stdio.h>
 
 #include <atomic>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 #include "fqkv_decode.h"
 #include "kv_formats.h"
@@ -37,18 +40,60 @@ int hip_fail(hipError_t e, const char* what) {
 
 bool aligned(const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; }
 
-// Split merge: in-kernel (arrival counters; one kernel per call) unless
-// forced to the two-kernel form or the call has too many head groups.
-std::atomic<int> g_force_two_kernel{0};
-std::atomic<unsigned> g_slot_ticket{0};
+constexpr int MAX_DEV = 64;
 
-int merge_slot(int64_t groups) {
+// Split merge: in-kernel (one kernel per call) unless forced to the
+// two-kernel form, the call does not fit a slot, or no slot is free.
+//
+// A slot (a set of arrival counters, one per device) may serve only calls
+// that never run at the same time, because the kernel of a call leaves its
+// counters at zero only when it ends. Calls on one stream run in order, so
+// each stream keeps one slot for its eager calls (EAGER_SLOTS of them, first
+// come first served), and each stream capture takes a slot of its own that
+// eager calls never use (the captured graph replays that slot, so two
+// replays of one graph must not overlap -- they would share the caller's
+// scratch and output too). Streams or captures beyond the free slots, and the
+// per-thread default stream (one handle for many streams), get the
+// two-kernel merge, which uses no library state.
+std::atomic<int> g_force_two_kernel{0};
+constexpr int EAGER_SLOTS = 12;  // slots 0 .. 11 for eager calls, 12 .. 15 for captures
+
+struct SlotTable {
+  std::mutex mu;
+  std::vector<std::pair<hipStream_t, int>> eager;
+  std::vector<std::pair<unsigned long long, int>> captured;
+};
+SlotTable g_slot_tables[MAX_DEV];
+
+int merge_slot(hipStream_t st, int64_t groups) {
   if (g_force_two_kernel.load(std::memory_order_relaxed) || groups > MAX_SPLIT_GROUPS) return -1;
-  return (int)(g_slot_ticket.fetch_add(1, std::memory_order_relaxed) % SPLIT_SLOTS);
+  if (st == hipStreamPerThread) return -1;
+  int dev = 0;
+  if (st ? hipStreamGetDevice(st, &dev) != hipSuccess : hipGetDevice(&dev) != hipSuccess) return -1;
+  if (dev < 0 || dev >= MAX_DEV) return -1;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  if (hipStreamGetCaptureInfo(st, &cs, &id) != hipSuccess) return -1;
+  SlotTable& t = g_slot_tables[dev];
+  std::lock_guard<std::mutex> lock(t.mu);
+  if (cs == hipStreamCaptureStatusActive) {
+    for (const auto& e : t.captured)
+      if (e.first == id) return e.second;
+    if ((int)t.captured.size() >= SPLIT_SLOTS - EAGER_SLOTS) return -1;
+    const int slot = EAGER_SLOTS + (int)t.captured.size();
+    t.captured.emplace_back(id, slot);
+    return slot;
+  }
+  if (cs != hipStreamCaptureStatusNone) return -1;  // invalidated capture: the launch fails anyway
+  for (const auto& e : t.eager)
+    if (e.first == st) return e.second;
+  if ((int)t.eager.size() >= EAGER_SLOTS) return -1;
+  const int slot = (int)t.eager.size();
+  t.eager.emplace_back(st, slot);
+  return slot;
 }
 
 // CU count per device, queried once (256 on MI355X).
-constexpr int MAX_DEV = 64;
 std::atomic<int> g_cus[MAX_DEV];
 
 int device_cus(int* out) {
@@ -178,7 +223,7 @@ int run_decode(int fmt, const void* q, const void* K, const void* V, const void*
     p.m_part = f;
     p.l_part = f + heads * S;
     p.o_part = f + acc_offset_floats(heads, S);
-    p.slot = merge_slot(rows * ngroups);
+    p.slot = merge_slot(st, rows * ngroups);
   }
   // With four or more work items per CU, workgroups of 4 waves: several
   // share a CU and hide each other's memory latency (measured on MI355X, MHA
@@ -268,7 +313,7 @@ int sk_fast(int fmt, const void* q, const void* K, const void* V, const void* Ks
   set_contiguous_layout(p, Hkv, N, (int)row_bytes_of(fmt, D));
   // S == 1 still writes the scratch (the caller asked for it); one split needs
   // no merge beyond the workgroup's own, done by the two-kernel path's combine.
-  p.slot = S > 1 ? merge_slot(Hkv * ngroups) : -1;
+  p.slot = S > 1 ? merge_slot(st, Hkv * ngroups) : -1;
   hipError_t e;
   if (ev_begin && (e = hipEventRecord((hipEvent_t)ev_begin, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
   e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)W, st);

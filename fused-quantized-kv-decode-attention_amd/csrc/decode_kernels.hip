@@ -50,6 +50,23 @@ namespace fqkv {
 
 constexpr float LOG2E = 1.4426950408889634f;
 
+// Timeline instrumentation, compiled in only with -DFQKV_TIMELINE: lane 0 of
+// each wave records the 100 MHz real-time counter at the kernel's stages into
+// g_timeline[workgroup][wave][stage] (for a host-side harness to read back).
+#ifdef FQKV_TIMELINE
+constexpr int TIMELINE_BLOCKS = 4096;
+__device__ unsigned long long g_timeline[TIMELINE_BLOCKS][NW_MAX][16];
+#define FQKV_STAMP(stage)                                                                          \
+  do {                                                                                             \
+    if ((threadIdx.x & 63) == 0 && blockIdx.x < TIMELINE_BLOCKS)                                   \
+      g_timeline[blockIdx.x][threadIdx.x >> 6][stage] = __builtin_amdgcn_s_memrealtime();          \
+  } while (0)
+#else
+#define FQKV_STAMP(stage) \
+  do {                    \
+  } while (0)
+#endif
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Row exchanges between the four 16-lane rows of a wave (all VALU):
@@ -195,20 +212,27 @@ __device__ __forceinline__ auto pick(uint32_t m1, uint32_t m2, Fn f) {
 // Merge S split partials for query heads h0 .. h0+nh-1:
 // o[h] = sum_s e^(m_s - M) acc_s / sum_s e^(m_s - M) l_s
 // (decode_attn_gqa_sk_fast.cu:57-94; m in natural-log units, an empty split
-// has m = -inf, l = 0, acc = 0 and weight 0).
+// has m = -inf, l = 0, acc = 0 and weight 0; an empty sequence, where every
+// split is empty, gives zeros).
 //
-// A unit is one head's 64-dim block; one wave merges one unit: lane s owns the
-// weight of split s of each 64-split block (kept in the wave's own LDS row, so
-// no barrier is needed to share it) and lane d accumulates output dim d over
-// the splits, with up to 64 partial loads in flight. Buffer descriptors bound
-// every load (reads past the last split return zero), so no lane computes a
-// bounds test per load. The m and l loads go out before the first partial
-// chunk, so a merge costs about one memory round trip (two when S > 64).
-// When there are fewer units than waves, the splits of a unit are cut into
-// nsl slices on different waves and the slices meet in LDS (the only
-// barrier; its condition is the same for the whole workgroup). With at most
-// CHK splits and no more units than waves everything is one chunk per wave,
-// and a short path skips the slice bookkeeping.
+// A unit is one head's 64-dim block; one wave merges one unit. Lane s forms
+// the weight of split s of each 64-split block (kept in the wave's own LDS
+// row, so no barrier is needed to share it); the partials arrive as 16-byte
+// loads, lane (k, q) = (lane / 16, lane % 16) reading dims 4q .. 4q+3 of
+// split 4j + k with load j, so a chunk of 32 splits is 8 loads per lane. A
+// CU issues a vector memory instruction every ~16 cycles whatever its width,
+// so 4-byte loads (one dim per lane) made the merge's loads, not its
+// latency, the cost: 34 of them per wave took ~1.8 us per merge on MI355X.
+// The four lane rows' sums are then added across rows. Buffer descriptors
+// end at the last split (the whole byte offset is the VGPR offset, which the
+// raw-buffer range check covers), so loads past it return zero and no lane
+// tests bounds per load. The m and l loads go out with the first chunk, so a
+// merge of up to 32 splits is one memory round trip. When there are fewer
+// units than waves, the splits of a unit are cut into nsl slices on different
+// waves that meet in LDS (the merge's only barrier; its condition is the same
+// for the whole workgroup). With at most CHK splits and no more units than
+// waves everything is one chunk per wave, and a short path skips the slice
+// bookkeeping.
 // CPOL: cache policy of the partial loads (CPOL_SC1 for partials that other
 // workgroups of the same launch stored at device scope).
 // s_w: 64 floats per wave (16-byte aligned rows); s_red: 65 floats per wave.
@@ -217,17 +241,29 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
                                              const float* __restrict__ o_part, _Float16* __restrict__ o,
                                              size_t h0, int nh, int S, float (*s_w)[64], float (*s_red)[65]) {
   constexpr int DB = D / 64;  // units per head
-  constexpr int CHK = 32;     // partial loads per lane per chunk
+  constexpr int CHK = 32;     // splits per chunk: 8 loads of 4 splits per lane
+  constexpr int NJ = CHK / 4;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nw = blockDim.x >> 6;
   const int units = nh * DB;
+  const int kr = lane >> 4;                          // split within a load: 4 j + kr
+  const uint32_t qo = 16u * (uint32_t)(lane & 15);   // byte offset of dims 4q .. 4q+3 in the unit
   auto ld = [](rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, CPOL));
   };
-  // partial loads: lane offset in a VGPR, the split's row offset as a scalar
-  auto ldo = [](rsrc_t r, uint32_t lane_off, uint32_t row_off) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)lane_off, (int)row_off, CPOL));
+  auto ld4 = [](rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(fl4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, CPOL));
+  };
+  // after the row sums every lane row holds the unit's 64 sums; lane (k, q)
+  // writes dim 4q + k, so one 2-byte store per lane covers the unit
+  auto emit = [&](fl4_t a, float L, _Float16* dst) {
+    a.x = rows4_sum(a.x);
+    a.y = rows4_sum(a.y);
+    a.z = rows4_sum(a.z);
+    a.w = rows4_sum(a.w);
+    const float v = kr == 0 ? a.x : (kr == 1 ? a.y : (kr == 2 ? a.z : a.w));
+    dst[4 * (lane & 15) + kr] = L > 0.0f ? (_Float16)(v / L) : (_Float16)0.0f;
   };
   if (S <= CHK && units <= nw) {
     // One chunk per unit and a wave per unit (the batch-1 split-K case):
@@ -239,28 +275,26 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
       const rsrc_t rM = make_rsrc(m_part + hrow * S, (uint32_t)S * 4u);
       const rsrc_t rL = make_rsrc(l_part + hrow * S, (uint32_t)S * 4u);
       const rsrc_t rO = make_rsrc(o_part + hrow * S * D + (wv - h * DB) * 64, (uint32_t)(S - 1) * D * 4u + 256u);
-      const uint32_t lo4 = (uint32_t)lane * 4u;
-      const float m0 = ld(rM, lo4);
-      const float l0 = ld(rL, lo4);
-      float ov[CHK];
+      const float m0 = ld(rM, 4u * (uint32_t)lane);
+      const float l0 = ld(rL, 4u * (uint32_t)lane);
+      fl4_t ov[NJ];
 #pragma unroll
-      for (int k = 0; k < CHK; ++k) ov[k] = ldo(rO, lo4, (uint32_t)(k * D * 4));  // zero past split S - 1
+      for (int j = 0; j < NJ; ++j) ov[j] = ld4(rO, (uint32_t)((4 * j + kr) * D * 4) + qo);  // zero past split S - 1
       float M = wave_max(lane < S ? m0 : -INFINITY);
       if (M == -INFINITY) M = 0.0f;  // every split empty: all weights 0
       const float w = lane < S ? fast_exp2((m0 - M) * LOG2E) : 0.0f;
       s_w[wv][lane] = w;
       const float L = wave_sum(w * l0);
-      const fl4_t* w4 = reinterpret_cast<const fl4_t*>(&s_w[wv][0]);
       fl4_t acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int k = 0; k < CHK / 4; ++k) {
-        const fl4_t wk = w4[k];
-        acc4.x = fmaf(wk.x, ov[4 * k], acc4.x);
-        acc4.y = fmaf(wk.y, ov[4 * k + 1], acc4.y);
-        acc4.z = fmaf(wk.z, ov[4 * k + 2], acc4.z);
-        acc4.w = fmaf(wk.w, ov[4 * k + 3], acc4.w);
+      for (int j = 0; j < NJ; ++j) {
+        const float wk = s_w[wv][4 * j + kr];
+        acc4.x = fmaf(wk, ov[j].x, acc4.x);
+        acc4.y = fmaf(wk, ov[j].y, acc4.y);
+        acc4.z = fmaf(wk, ov[j].z, acc4.z);
+        acc4.w = fmaf(wk, ov[j].w, acc4.w);
       }
-      o[hrow * D + (wv - h * DB) * 64 + lane] = (_Float16)(((acc4.x + acc4.y) + (acc4.z + acc4.w)) / L);
+      emit(acc4, L, o + hrow * D + (wv - h * DB) * 64);
     }
     return;
   }
@@ -278,21 +312,22 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
     const int start = sl * len;
     const int end = min(S, start + len);
     const bool live = (wv >> lg) < cu && u < units && start < end;  // wave-uniform
-    float acc = 0.0f, L = 0.0f;
+    fl4_t acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    float L = 0.0f;
     if (live) {
       const size_t hrow = h0 + h;
       const rsrc_t rM = make_rsrc(m_part + hrow * S, (uint32_t)S * 4u);
       const rsrc_t rL = make_rsrc(l_part + hrow * S, (uint32_t)S * 4u);
-      // split start + k, dim lane at byte (k D + lane) 4; the record ends with
-      // the last split's 64 dims
+      // split start + i, dims 4q .. 4q+3 at byte i D 4 + qo; the record ends
+      // with the slice's last split's 64 dims
       const rsrc_t rO = make_rsrc(o_part + (hrow * S + start) * D + db * 64,
                                   (uint32_t)(end - start - 1) * D * 4u + 256u);
       const uint32_t lo4 = (uint32_t)lane * 4u;
       const float m0 = ld(rM, lo4);
       const float l0 = ld(rL, lo4);
-      float ov[CHK];
+      fl4_t ov[NJ];
 #pragma unroll
-      for (int k = 0; k < CHK; ++k) ov[k] = ldo(rO, lo4, (uint32_t)(k * D * 4));
+      for (int j = 0; j < NJ; ++j) ov[j] = ld4(rO, (uint32_t)((4 * j + kr) * D * 4) + qo);
       float M = lane < S ? m0 : -INFINITY;
       for (int s0 = 64; s0 < S; s0 += 64) {
         const float mm = ld(rM, lo4 + (uint32_t)s0 * 4u);
@@ -300,19 +335,6 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
       }
       M = wave_max(M);
       if (M == -INFINITY) M = 0.0f;  // every split empty: all weights 0
-      // four independent sums, so the FMAs do not wait on each other
-      fl4_t acc4 = {0.0f, 0.0f, 0.0f, 0.0f};
-      auto accumulate = [&](int c0) {
-        const fl4_t* w4 = reinterpret_cast<const fl4_t*>(&s_w[wv][c0 & 63]);
-#pragma unroll
-        for (int k = 0; k < CHK / 4; ++k) {
-          const fl4_t wk = w4[k];
-          acc4.x = fmaf(wk.x, ov[4 * k], acc4.x);
-          acc4.y = fmaf(wk.y, ov[4 * k + 1], acc4.y);
-          acc4.z = fmaf(wk.z, ov[4 * k + 2], acc4.z);
-          acc4.w = fmaf(wk.w, ov[4 * k + 3], acc4.w);
-        }
-      };
       for (int c0 = start; c0 < end; c0 += CHK) {
         const int b = c0 >> 6;
         if (c0 == start || (c0 & 63) == 0) {  // weights of splits 64 b .. 64 b + 63 in this slice
@@ -326,35 +348,53 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
           L = fmaf(w, ll, L);
           s_w[wv][lane] = w;
         }
+        auto accumulate = [&](const fl4_t (&v)[NJ]) {
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) {
+            const float wk = s_w[wv][(c0 & 63) + 4 * j + kr];
+            acc4.x = fmaf(wk, v[j].x, acc4.x);
+            acc4.y = fmaf(wk, v[j].y, acc4.y);
+            acc4.z = fmaf(wk, v[j].z, acc4.z);
+            acc4.w = fmaf(wk, v[j].w, acc4.w);
+          }
+        };
         const int c1 = c0 + CHK;
         if (c1 < end) {
-          float nv[CHK];
+          fl4_t nv[NJ];
 #pragma unroll
-          for (int k = 0; k < CHK; ++k) nv[k] = ldo(rO, lo4, (uint32_t)((c1 - start + k) * D * 4));
-          accumulate(c0);
+          for (int j = 0; j < NJ; ++j) nv[j] = ld4(rO, (uint32_t)((c1 - start + 4 * j + kr) * D * 4) + qo);
+          accumulate(ov);
 #pragma unroll
-          for (int k = 0; k < CHK; ++k) ov[k] = nv[k];
+          for (int j = 0; j < NJ; ++j) ov[j] = nv[j];
         } else {
-          accumulate(c0);
+          accumulate(ov);
         }
       }
-      acc = (acc4.x + acc4.y) + (acc4.z + acc4.w);
       L = wave_sum(L);
     }
     if (nsl > 1) {
+      // slices meet in LDS: the row sums first, then lane (k, q) parks dim 4q + k
       if (live) {
-        s_red[wv][lane] = acc;
+        acc4.x = rows4_sum(acc4.x);
+        acc4.y = rows4_sum(acc4.y);
+        acc4.z = rows4_sum(acc4.z);
+        acc4.w = rows4_sum(acc4.w);
+        s_red[wv][4 * (lane & 15) + kr] = kr == 0 ? acc4.x : (kr == 1 ? acc4.y : (kr == 2 ? acc4.z : acc4.w));
         if (lane == 0) s_red[wv][64] = L;
       }
       __syncthreads();
-      if (live && sl == 0)
+      if (live && sl == 0) {
+        float a = s_red[wv][lane];
         for (int q = 1; q < nsl; ++q) {
           if ((q * len) >= S) break;  // empty slice
-          acc += s_red[wv + q][lane];
+          a += s_red[wv + q][lane];
           L += s_red[wv + q][64];
         }
+        o[(h0 + h) * D + db * 64 + lane] = L > 0.0f ? (_Float16)(a / L) : (_Float16)0.0f;
+      }
+    } else if (live) {
+      emit(acc4, L, o + (h0 + h) * D + db * 64);
     }
-    if (live && sl == 0) o[(h0 + h) * D + db * 64 + lane] = (_Float16)(acc / L);
   }
 }
 
@@ -397,7 +437,7 @@ __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const f
     }
     const size_t qh = qrow0 + h;
     if (p.direct) {
-      p.o[qh * D + d] = (_Float16)(O / L);
+      p.o[qh * D + d] = L > 0.0f ? (_Float16)(O / L) : (_Float16)0.0f;  // an empty sequence gives zeros
     } else {
       const size_t b = qh * p.S + s;
       float* orow = p.o_part + b * D;
@@ -432,7 +472,9 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   __shared__ __attribute__((aligned(16))) float s_mw[NW_MAX][64];  // in-kernel split merge
   __shared__ float s_mr[NW_MAX][65];
   __shared__ int s_last;
+  extern __shared__ __attribute__((aligned(16))) uint8_t s_kstage[];  // fp16 K staging, F::KSTAGE bytes per wave
 
+  FQKV_STAMP(0);  // start
   const int lane = threadIdx.x & 63;
   // wave index as a scalar, so tile loops branch per wave, not per lane
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -504,7 +546,13 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   const rsrc_t rV = make_rsrc(Vr, PAGED ? 0u : (uint32_t)hi * ts);
   const rsrc_t rKs = make_rsrc(Ksr, PAGED ? 0u : (uint32_t)hi * sts);
   const rsrc_t rVs = make_rsrc(Vsr, PAGED ? 0u : (uint32_t)hi * sts);
-  const uint32_t koff = (uint32_t)n * ts + F::klane(R);
+  // K loads: operand-A layout straight from memory, or (fp16) whole rows
+  // that go through the wave's LDS rows
+  uint32_t koff;
+  if constexpr (F::STAGE_K)
+    koff = F::krow_lane(lane, ts);
+  else
+    koff = (uint32_t)n * ts + F::klane(R);
   const uint32_t voff = (uint32_t)R * ts + (uint32_t)n * VG::VBYTES;
   // tile t's sources: descriptors and the byte offset of its first token
   struct TileSrc {
@@ -572,7 +620,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     for (int u = 0; u < U; ++u) src[u] = tile_src(pb + u * step);
     const bool full = !PAGED && pb + (U - 1) * step + 16 <= hi;  // every token of the pass is before hi
 #pragma unroll
-    for (int u = 0; u < U; ++u) F::load_k(src[u].k, src[u].off + koff, kr[u]);
+    for (int u = 0; u < U; ++u) {
+      if constexpr (F::STAGE_K)
+        F::load_k_rows(src[u].k, src[u].off + koff, ts, kr[u]);
+      else
+        F::load_k(src[u].k, src[u].off + koff, kr[u]);
+    }
     if constexpr (F::QUANT) {
       if constexpr (!PAGED) {
         if (vec_sc && full) {
@@ -628,6 +681,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       for (int j = 0; j < 4; ++j) load_vchunk<VG::VBYTES, VD>(src[u].v, base + (uint32_t)(4 * j) * ts, vr[u][j]);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
+    FQKV_STAMP(1);                      // the pass's loads issued
 
     if constexpr (PICK_SC) {
 #pragma unroll
@@ -643,6 +697,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     f4_t c4[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
+      if constexpr (F::STAGE_K) F::stage_k(s_kstage + w * F::KSTAGE, lane, kr[u]);
       c4[u] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int i = 0; i < F::NKI; ++i)
@@ -737,6 +792,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       for (int c = 0; c < VE; ++c) acc[c] *= acc_alpha;
     }
     m_run = mn;
+    FQKV_STAMP(2);  // scores and weights of the pass (its K has arrived)
     // Two tiles per product: v_mfma_f32_16x16x32_f16 contracts over 32
     // operand slots, lane row R's slots 8R .. 8R+3 taking tokens 4R .. 4R+3
     // of tile u and 8R+4 .. 8R+7 the same tokens of tile u + 1 (half the
@@ -773,6 +829,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     }
   }
 
+  FQKV_STAMP(3);  // last pass's P.V products issued
   // ---- wave totals: l over the four lane rows; O^T rows are disjoint; the
   // P columns of a head add up (same running max and shift in all of them) ----
   if constexpr (F::QUANT) l_run = __builtin_amdgcn_ldexpf(l_run, -acc_shift);
@@ -802,7 +859,9 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       s_l[n][w] = l_run;
     }
   }
+  FQKV_STAMP(4);  // wave totals written to LDS
   __syncthreads();
+  FQKV_STAMP(5);  // wave-merge barrier passed
 
   // ---- merge the waves, emit output or split scratch ----
   if (nw == 8)
@@ -820,6 +879,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // visible device-wide. The last arriver reads every partial with
   // device-scope loads. No L2 writeback or invalidate is needed, and nobody
   // waits on the counter, so no workgroup can stall.
+  FQKV_STAMP(6);  // output or partials issued
   if (!p.direct && p.slot >= 0) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -828,13 +888,16 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       s_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.S - 1;
     }
     __syncthreads();
+    FQKV_STAMP(7);  // arrival known
     if (s_last) {
       merge_splits<D, CPOL_SC1>(p.m_part, p.l_part, p.o_part, p.o, qrow0, hcnt, p.S, s_mw, s_mr);
+      FQKV_STAMP(9);  // merge done
       // every workgroup of the group has counted in: reset for the next call
       if (threadIdx.x == 0)
         __hip_atomic_store(arrival_counter(p.slot, wsg), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+  FQKV_STAMP(10);  // end
 }
 
 // Two-kernel form of the split merge (decode_attn_gqa_sk_fast.cu:57-94): one
@@ -888,10 +951,12 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
 // ------------------------------------------------------------ launchers ----
 template <int FMT, int D, int HG>
 static hipError_t launch_partial_t(const PartialParams& p, int nblocks, int nw, hipStream_t st) {
+  size_t lds = 0;
+  if constexpr (Fmt<FMT, D>::STAGE_K) lds = (size_t)nw * Fmt<FMT, D>::KSTAGE;
   if (p.page_table)
-    hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, true>), dim3(nblocks), dim3(64 * nw), 0, st, p);
+    hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, true>), dim3(nblocks), dim3(64 * nw), lds, st, p);
   else
-    hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false>), dim3(nblocks), dim3(64 * nw), 0, st, p);
+    hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false>), dim3(nblocks), dim3(64 * nw), lds, st, p);
   return hipGetLastError();
 }
 
