@@ -311,15 +311,15 @@ int sk_fast(int fmt, const void* q, const void* K, const void* V, const void* Ks
   p.o = (_Float16*)o;
   p.direct = 0;
   set_contiguous_layout(p, Hkv, N, (int)row_bytes_of(fmt, D));
-  // S == 1 still writes the scratch (the caller asked for it); one split needs
-  // no merge beyond the workgroup's own, done by the two-kernel path's combine.
+  // S == 1 still writes the scratch (the caller asked for it); with one split
+  // the partial kernel also writes the output, and no merge is launched.
   p.slot = S > 1 ? merge_slot(st, Hkv * ngroups) : -1;
   hipError_t e;
   if (ev_begin && (e = hipEventRecord((hipEvent_t)ev_begin, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
   e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)W, st);
   if (e != hipSuccess) return hip_fail(e, "partial");
   if (ev_end && (e = hipEventRecord((hipEvent_t)ev_end, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-  if (p.slot < 0) {
+  if (S > 1 && p.slot < 0) {
     e = launch_combine((int)D, m_part, l_part, o_part, o, (int)Hq, (int)S, (int)CW, st);
     if (e != hipSuccess) return hip_fail(e, "combine");
   }

@@ -257,13 +257,16 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
   };
   // after the row sums every lane row holds the unit's 64 sums; lane (k, q)
   // writes dim 4q + k, so one 2-byte store per lane covers the unit
+  auto put = [&](_Float16* unit, int i, float v, float L) {  // output dim i of a 64-dim unit
+    unit[i] = L > 0.0f ? (_Float16)(v / L) : (_Float16)0.0f;
+  };
   auto emit = [&](fl4_t a, float L, _Float16* dst) {
     a.x = rows4_sum(a.x);
     a.y = rows4_sum(a.y);
     a.z = rows4_sum(a.z);
     a.w = rows4_sum(a.w);
     const float v = kr == 0 ? a.x : (kr == 1 ? a.y : (kr == 2 ? a.z : a.w));
-    dst[4 * (lane & 15) + kr] = L > 0.0f ? (_Float16)(v / L) : (_Float16)0.0f;
+    put(dst, 4 * (lane & 15) + kr, v, L);
   };
   if (S <= CHK && units <= nw) {
     // One chunk per unit and a wave per unit (the batch-1 split-K case):
@@ -390,7 +393,7 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
           a += s_red[wv + q][lane];
           L += s_red[wv + q][64];
         }
-        o[(h0 + h) * D + db * 64 + lane] = L > 0.0f ? (_Float16)(a / L) : (_Float16)0.0f;
+        put(o + (h0 + h) * D + db * 64, lane, a, L);
       }
     } else if (live) {
       emit(acc4, L, o + (h0 + h) * D + db * 64);
@@ -455,6 +458,9 @@ __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const f
         }
         orow[d] = O;
       }
+      // one split: the workgroup holds the whole result, so it writes the
+      // output too and no merge follows (one launch per call)
+      if (p.S == 1) p.o[qh * D + d] = L > 0.0f ? (_Float16)(O / L) : (_Float16)0.0f;
     }
   }
 }
@@ -681,7 +687,6 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       for (int j = 0; j < 4; ++j) load_vchunk<VG::VBYTES, VD>(src[u].v, base + (uint32_t)(4 * j) * ts, vr[u][j]);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
-    FQKV_STAMP(1);                      // the pass's loads issued
 
     if constexpr (PICK_SC) {
 #pragma unroll
@@ -792,7 +797,6 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       for (int c = 0; c < VE; ++c) acc[c] *= acc_alpha;
     }
     m_run = mn;
-    FQKV_STAMP(2);  // scores and weights of the pass (its K has arrived)
     // Two tiles per product: v_mfma_f32_16x16x32_f16 contracts over 32
     // operand slots, lane row R's slots 8R .. 8R+3 taking tokens 4R .. 4R+3
     // of tile u and 8R+4 .. 8R+7 the same tokens of tile u + 1 (half the

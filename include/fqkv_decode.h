@@ -9,6 +9,8 @@
  * allocates device memory (callers pass any workspace; the library's only
  * device state is a static array of split-merge arrival counters).
  *
+ * An empty sequence (a paged batch slot with seq_len <= 0) yields zeros.
+ *
  * Data formats (the reference's layouts, unchanged):
  *   fp16 KV        K, V: [rows, N, D] __half, row-major
  *   int8 KV        K, V: [rows, N, D] int8, per-token scales Ks, Vs: [rows, N] __half
@@ -118,6 +120,7 @@ int fqkv_decode_attn_gqa(const void* q, const void* K, const void* V, void* o, i
  * sum exp(score - m) V; an empty split stores (-inf, 0, 0).
  * A batch folds into the head axis: q [B*Hq, D], K [B*Hkv, N, D].
  * W in {2, 4, 8} waves per partial workgroup, CW in {4, 8} combine waves.
+ * With S = 1 the partial kernel writes the output as well (one launch).
  * Replaces gqa_sk_fast(q, K, V, m_part, l_part, o_part, o, S, W, CW)
  * (kernels/decode_attn_gqa_sk_fast.cu:95-112).
  */
@@ -247,11 +250,15 @@ int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, v
  * Split merge mode for calls that split the sequence (gqa_sk_fast with S > 1
  * and the internal splits of the single-block entry points). Default (0):
  * one kernel per call; the last workgroup of each head group to finish merges
- * that group's split partials, using library-owned arrival counters (16
- * slots taken round-robin per call, so up to 16 such calls may run
- * concurrently on different streams; calls that replay one captured graph
- * concurrently share a slot and must not overlap). 1: a partial kernel then
- * a separate combine kernel, as the reference launches them
+ * that group's split partials, using library-owned arrival counters. The
+ * counters come in 16 slots per device: each stream keeps one of 12 slots for
+ * its eager calls (first come, first served), and each stream capture takes
+ * one of the other 4 for the graph it records; calls on a stream or capture
+ * with no free slot, and calls on hipStreamPerThread, use the two-kernel
+ * merge. So calls that may overlap never share a slot; the one exception a
+ * caller must avoid is replaying one captured graph on two streams at once
+ * (those replays also share the caller's scratch and output). 1: a partial
+ * kernel then a separate combine kernel, as the reference launches them
  * (decode_attn_gqa_sk_fast.cu:100-111). Results agree to fp32 rounding.
  * Process-wide; returns FQKV_OK.
  */

@@ -195,3 +195,22 @@ def test_strided_rejects_bad_views():
     with pytest.raises(RuntimeError, match="strides"):  # token stride not a multiple of 16 bytes
         Kb = torch.zeros(1, 2, 40, 68, dtype=torch.float16, device="cuda")[..., :64]
         fq.decode_attn_gqa_strided(q, Kb, Kb, 8)
+
+
+@pytest.mark.parametrize("fmt", ["fp16", "int8", "int4"])
+@pytest.mark.parametrize("lens", [[0, 5, 0, 300], [0, 20000, 0]])
+def test_paged_empty_sequences_give_zeros(fmt, lens):
+    """A batch slot with seq_len 0 (continuous batching) has no keys: its output
+    is defined as zeros, in the single-pass and in the split path alike, and
+    its neighbours are unaffected."""
+    g = torch.Generator().manual_seed(56)
+    Hq, Hkv, D = 32, 8, 128
+    Kp, Vp, Ks, Vs, table, sl, seqs = paged_cache(g, lens, Hkv, D, 32, fmt)
+    q = draw(g, len(lens), Hq, D).half()
+    out = fq.decode_attn_gqa_paged(q.cuda(), Kp, Vp, table, sl, max(lens), 8, Ks, Vs)
+    for b, (Kb, Vb) in enumerate(seqs):
+        if lens[b] == 0:
+            assert torch.equal(out[b].cpu(), torch.zeros(Hq, D, dtype=torch.float16)), b
+        else:
+            ref = oracle.gqa_attention(q.numpy()[b:b + 1], Kb[None], Vb[None])[0]
+            assert maxerr(out[b], ref) <= TOL, (b, lens[b])

@@ -131,3 +131,31 @@ def test_gpu_quantize_append_writes_only_its_slots(dtype, D, fmt):
         pos += n
     with pytest.raises(RuntimeError, match="pos"):
         fq.quantize_kv_append_(Kn[:, :, :1].contiguous(), Vn[:, :, :1].contiguous(), Kc, Vc, Ksc, Vsc, cap)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_reference_quantizer_expressions_on_gpu_match_oracle(dtype, fmt):
+    """The reference quantizes with PyTorch expressions on its device tensors,
+    written with a division by the Python scalar 127.0 or 7.0
+    (tests/test_kernels.py:32-34, nb:292-299). Those expressions, evaluated as
+    written on this GPU's PyTorch, give exactly the oracle's bytes and fp16
+    scales; the oracle rounds the scale as max|x| * fp32(1/qmax), the form
+    PyTorch's division by a scalar takes."""
+    qmax = 127 if fmt == "int8" else 7
+    D = 128
+    g = torch.Generator().manual_seed(31)
+    X = torch.randn(2, 4000, D, generator=g).to(dtype)
+    X = torch.cat([X.reshape(-1, D), torch.from_numpy(edge_rows(D, X.numpy().dtype))]).contiguous()
+    Xd = X.cuda()
+    a = Xd.abs().amax(-1, keepdim=True)
+    s = (a / float(qmax)).clamp(min=1e-8)
+    qv = torch.clamp(torch.round(Xd / s), -qmax, qmax).to(torch.int8)
+    if fmt == "int4":
+        qv = qv.view(qv.shape[0], D // 2, 2)
+        qv = ((qv[..., 0] & 0xF) | ((qv[..., 1] & 0xF) << 4)).to(torch.uint8)
+        oq, os_ = oracle.quant_int4_per_token(X.numpy())
+    else:
+        oq, os_ = oracle.quant_int8_per_token(X.numpy())
+    np.testing.assert_array_equal(qv.cpu().numpy(), oq)
+    np.testing.assert_array_equal(s.squeeze(-1).half().cpu().numpy().view(np.uint16), os_.view(np.uint16))

@@ -1,0 +1,151 @@
+"""The in-kernel split merge under concurrency and at the edges of its buffers
+(needs an MI355X).
+
+The last workgroup of each (KV row, head group) to finish merges the group's
+split partials; it learns that it is last from an arrival counter in a slot of
+library-owned counters. Each stream keeps a slot for its eager calls and each
+stream capture gets one of its own, so calls that may run at the same time
+never share one; calls beyond the free slots take the two-kernel merge. These
+tests run captured graphs beside eager calls, more streams than slots, and
+partials whose neighbouring memory holds NaN, and check every output against
+the same call run alone (bit for bit) or against the oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import fqkv_decode as fq
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+DEV = "cuda"
+
+
+def draw(g, *shape):
+    return torch.randn(*shape, generator=g, dtype=torch.float32)
+
+
+def make_call(g, Hq=32, Hkv=8, N=3000, D=128, S=24):
+    q, K, V = draw(g, Hq, D).half().to(DEV), draw(g, Hkv, N, D).half().to(DEV), draw(g, Hkv, N, D).half().to(DEV)
+    scratch = (torch.empty(Hq, S, device=DEV), torch.empty(Hq, S, device=DEV), torch.empty(Hq, S, D, device=DEV))
+    o = torch.empty(Hq, D, dtype=torch.float16, device=DEV)
+    return q, K, V, scratch, o, S
+
+
+def run(call):
+    q, K, V, (mp, lp, op), o, S = call
+    fq.gqa_sk_fast(q, K, V, mp, lp, op, o, S, 8, 8)
+
+
+def test_graph_replays_beside_eager_calls_on_a_side_stream():
+    """A captured split-K graph replayed on one stream while eager split calls
+    run on another: the capture holds a slot of its own, so both stay equal
+    to their solo results; afterwards solo calls on both streams are still
+    exact (no counter was left behind)."""
+    g = torch.Generator().manual_seed(60)
+    a = make_call(g)
+    b = make_call(g, Hq=64, Hkv=8, N=5000, S=32)
+    run(a)
+    ref_a = a[4].clone()
+    run(b)
+    ref_b = b[4].clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run(a)
+    sx, sy = torch.cuda.Stream(), torch.cuda.Stream()
+    for s in (sx, sy):
+        s.wait_stream(torch.cuda.current_stream())
+    for _ in range(20):
+        with torch.cuda.stream(sx):
+            graph.replay()
+        with torch.cuda.stream(sy):
+            run(b)
+    for s in (sx, sy):
+        torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(a[4], ref_a)
+    assert torch.equal(b[4], ref_b)
+    for s in (sx, sy):
+        with torch.cuda.stream(s):
+            a[4].zero_()
+            run(a)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        assert torch.equal(a[4], ref_a)
+
+
+def test_more_streams_than_merge_slots():
+    """Split calls in flight on 20 streams at once, more than there are eager
+    slots: streams beyond them merge with the two-kernel form, and every
+    output equals the same call run alone."""
+    g = torch.Generator().manual_seed(61)
+    calls = [make_call(g, N=1500, S=16) for _ in range(20)]
+    alone = []
+    for c in calls:
+        run(c)
+        alone.append(c[4].clone())
+        c[4].zero_()
+    streams = [torch.cuda.Stream() for _ in range(20)]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    for rep in range(3):
+        for c, s in zip(calls, streams):
+            with torch.cuda.stream(s):
+                run(c)
+    for s in streams:
+        torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for c, ref in zip(calls, alone):
+        assert torch.equal(c[4], ref)
+
+
+@pytest.mark.parametrize("S", [5, 17, 31, 32, 40])
+def test_merge_reads_stay_inside_the_partials(S, merge_mode):
+    """m_part, l_part and o_part are the leading views of NaN-filled buffers,
+    so any read past the last split would bring NaN (times a weight of 0
+    still NaN) into the output. The output must match the oracle."""
+    Hq, Hkv, N, D = 32, 8, 2500, 128
+    g = torch.Generator().manual_seed(62)
+    q, K, V = draw(g, Hq, D).half(), draw(g, Hkv, N, D).half(), draw(g, Hkv, N, D).half()
+    nan = float("nan")
+    mp = torch.full((Hq * S + 4096,), nan, device=DEV)[:Hq * S].view(Hq, S)
+    lp = torch.full((Hq * S + 4096,), nan, device=DEV)[:Hq * S].view(Hq, S)
+    op = torch.full((Hq * S * D + 65536,), nan, device=DEV)[:Hq * S * D].view(Hq, S, D)
+    o = torch.empty(Hq, D, dtype=torch.float16, device=DEV)
+    fq.gqa_sk_fast(q.to(DEV), K.to(DEV), V.to(DEV), mp, lp, op, o, S, 8, 8)
+    ref = oracle.gqa_attention(q.numpy()[None], K.numpy()[None], V.numpy()[None])[0]
+    out = o.float().cpu().numpy()
+    assert np.isfinite(out).all()
+    assert float(np.abs(out.astype(np.float64) - ref).max()) <= TOL
+
+
+def test_single_block_workspace_followed_by_nan(merge_mode):
+    """The C ABI's split workspace handed over as the leading bytes of a
+    NaN-filled buffer: the internal split merge reads only its partials."""
+    import ctypes
+
+    L = ctypes.CDLL(fq.lib_path())
+    I64, VP, SZ = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
+    L.fqkv_last_error.restype = ctypes.c_char_p
+    L.fqkv_workspace_bytes.restype = SZ
+    L.fqkv_workspace_bytes.argtypes = [I64, I64, I64, I64, ctypes.c_int, I64]
+    L.fqkv_decode_attn_gqa.argtypes = [VP] * 4 + [I64] * 6 + [VP, SZ, VP]
+    B, Hq, Hkv, N, D = 1, 32, 8, 9000, 128
+    n = L.fqkv_workspace_bytes(B * Hkv, Hq // Hkv, N, D, 0, 8)
+    assert n > 0
+    g = torch.Generator().manual_seed(63)
+    q, K, V = draw(g, B, Hq, D).half(), draw(g, B, Hkv, N, D).half(), draw(g, B, Hkv, N, D).half()
+    buf = torch.full(((n + (1 << 20)) // 4,), float("nan"), device=DEV)  # 1 MiB of NaN after the workspace
+    o = torch.empty(B, Hq, D, dtype=torch.float16, device=DEV)
+    qd, Kd, Vd = q.to(DEV), K.to(DEV), V.to(DEV)
+    rc = L.fqkv_decode_attn_gqa(qd.data_ptr(), Kd.data_ptr(), Vd.data_ptr(), o.data_ptr(), B, Hq, Hkv, N, D, 8,
+                                buf.data_ptr(), n, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, L.fqkv_last_error().decode()
+    torch.cuda.synchronize()
+    out = o.float().cpu().numpy()
+    assert np.isfinite(out).all()
+    ref = oracle.gqa_attention(q.numpy(), K.numpy(), V.numpy())
+    assert float(np.abs(out.astype(np.float64) - ref).max()) <= TOL

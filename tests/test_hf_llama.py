@@ -24,8 +24,8 @@ from fqkv_decode import hf_llama  # noqa: E402
 
 
 def tiny_llama(layers=4, hidden=512, heads=8, kv_heads=2, head_dim=64, vocab=1000, init=0.2, dtype=torch.float32,
-               device="cpu"):
-    cfg = transformers.LlamaConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=2 * hidden,
+               device="cpu", intermediate=None):
+    cfg = transformers.LlamaConfig(vocab_size=vocab, hidden_size=hidden, intermediate_size=intermediate or 2 * hidden,
                                    num_hidden_layers=layers, num_attention_heads=heads,
                                    num_key_value_heads=kv_heads, head_dim=head_dim,
                                    max_position_embeddings=8192, initializer_range=init,
@@ -89,12 +89,25 @@ def greedy(model, ids, steps):
     return toks, margins
 
 
+# Llama-3.2-1B's attention geometry (nb:966): 16 layers, 32 query / 8 KV
+# heads of 64, hidden 2048, MLP 8192, vocabulary 128256; random init at the
+# LlamaConfig default scale (no checkpoint is fetched). "small" is a 4-layer
+# model with 8 / 2 heads for a quick second geometry.
+GEOMETRIES = {
+    "llama32_1b": dict(layers=16, hidden=2048, heads=32, kv_heads=8, head_dim=64, vocab=128256, init=0.02,
+                       intermediate=8192),
+    "small": dict(),
+}
+
+
 @pytest.mark.gpu
+@pytest.mark.parametrize("geometry", sorted(GEOMETRIES))
 @pytest.mark.parametrize("ctx", [37, 3000])
-def test_gpu_decode_matches_sdpa(ctx):
+def test_gpu_decode_matches_sdpa(ctx, geometry):
     name = hf_llama.register()
-    model = tiny_llama(dtype=torch.float16, device="cuda")
-    ids = torch.randint(0, 1000, (1, ctx), generator=torch.Generator().manual_seed(2)).cuda()
+    model = tiny_llama(dtype=torch.float16, device="cuda", **GEOMETRIES[geometry])
+    vocab = model.config.vocab_size
+    ids = torch.randint(0, vocab, (1, ctx), generator=torch.Generator().manual_seed(2)).cuda()
     set_impl(model, "sdpa")
     base, margins = greedy(model, ids, 24)
     set_impl(model, name)
