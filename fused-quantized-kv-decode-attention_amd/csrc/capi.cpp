@@ -326,6 +326,48 @@ int sk_fast(int fmt, const void* q, const void* K, const void* V, const void* Ks
   return FQKV_OK;
 }
 
+// ---- the no-allocation split-K entry point's scratch ----
+//
+// fqkv_gqa_sk_fast_noalloc keeps the split partials (m, l, acc) that
+// fqkv_gqa_sk_fast takes from the caller in this file-scope device array
+// instead: NOALLOC_SCRATCH_BYTES per device, allocated when the code object
+// loads and held until the process ends. In host code `scratch` names a
+// host-side stand-in, not device memory, so its device address is looked up
+// once per device with hipGetSymbolAddress (with that device current) and
+// only that address is handed to kernels. Every call on a device shares the
+// device's array and leaves its last partials there; nothing in it has to
+// start at zero (the partial kernel writes every entry the merge reads).
+// Calls that overlap on one device race on it.
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(8) << 20;
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEV];
+
+int scratch_address(hipStream_t st, void** out) {
+  int dev = 0;
+  hipError_t e = st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "scratch: device of the stream");
+  if (dev < 0 || dev >= MAX_DEV) return fail(FQKV_ERR_HIP, "scratch: device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = 0;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_fail(e, "hipSetDevice");
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess && e2 != hipSuccess) e = e2;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!ptr) return fail(FQKV_ERR_HIP, "hipGetSymbolAddress(scratch) returned no address");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FQKV_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -420,6 +462,29 @@ int fqkv_gqa_sk_fast_timed(const void* q, const void* K, const void* V, float* m
                            void* ev_begin, void* ev_end) {
   return sk_fast(KV_F16, q, K, V, nullptr, nullptr, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW,
                  stream, ev_begin, ev_end);
+}
+
+int fqkv_gqa_sk_fast_noalloc(const void* q, const void* K, const void* V, void* o, int64_t Hq, int64_t Hkv,
+                             int64_t N, int64_t D, int64_t S, int64_t W, int64_t CW, void* stream) {
+  // the argument checks sk_fast makes before any HIP call, plus the scratch size
+  int rc = check_common(N, D, W);
+  if (rc) return rc;
+  if (S < 1 || S > (1 << 20)) return fail(FQKV_ERR_ARG, "S: split count must be in [1, 2^20], got %lld", (long long)S);
+  if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
+    return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
+  // m [Hq*S], l [Hq*S], then acc [Hq*S*D] from a 16-byte boundary
+  const size_t acc_off = (size_t)((2 * Hq * S + 3) & ~(int64_t)3) * sizeof(float);
+  const size_t need = acc_off + (size_t)Hq * (size_t)S * (size_t)D * sizeof(float);
+  if (need > NOALLOC_SCRATCH_BYTES)
+    return fail(FQKV_ERR_ARG, "S: %lld splits of %lld heads need %zu bytes of partials, more than the %zu-byte "
+                "no-allocation scratch; use fewer splits or fqkv_gqa_sk_fast", (long long)S, (long long)Hq, need,
+                NOALLOC_SCRATCH_BYTES);
+  if ((rc = check_ptrs_kv(q, K, V, o))) return rc;
+  void* base = nullptr;
+  if ((rc = scratch_address((hipStream_t)stream, &base))) return rc;
+  float* f = (float*)base;
+  return sk_fast(KV_F16, q, K, V, nullptr, nullptr, f, f + Hq * S, (float*)((char*)base + acc_off), o, Hq, Hkv, N, D,
+                 S, W, CW, stream, nullptr, nullptr);
 }
 
 int fqkv_decode_attn_gqa_quant(const void* q, const void* K, const void* V, const void* Ks,

@@ -129,6 +129,24 @@ int fqkv_gqa_sk_fast(const void* q, const void* K, const void* V, float* m_part,
                      int64_t S, int64_t W, int64_t CW, void* stream);
 
 /*
+ * fqkv_gqa_sk_fast without the caller's scratch: the same call, except that
+ * the fp32 split partials live in a file-scope device array of the library
+ * (8 MiB per device, held until the process ends) instead of caller-owned
+ * m_part / l_part / o_part, so a call allocates nothing -- for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). The partials need
+ * (2 * Hq * S rounded up to a multiple of 4 + Hq * S * D) * 4 bytes; a
+ * larger Hq * S is rejected (FQKV_ERR_ARG, message starting "S:") before
+ * any HIP call. Every call on a device shares that device's array and leaves
+ * its partials there; calls that overlap on one device (other streams, or a
+ * captured graph replayed beside them) race on it, so such calls must be
+ * ordered. Output, layouts and S / W / CW as for fqkv_gqa_sk_fast, and the
+ * result equals it bit for bit. No counterpart in the reference.
+ */
+int fqkv_gqa_sk_fast_noalloc(const void* q, const void* K, const void* V, void* o, int64_t Hq, int64_t Hkv,
+                             int64_t N, int64_t D, int64_t S, int64_t W, int64_t CW, void* stream);
+
+/*
  * GQA-aware decode over an int8 or int4 KV cache (kv_format FQKV_KV_I8 /
  * FQKV_KV_I4) with per-token fp16 scales: the GQA head mapping of
  * fqkv_decode_attn_gqa with the KV format of fqkv_decode_attn_int8_mw /
