@@ -587,6 +587,16 @@ int fqkv_decode_attn_gqa_paged(const void* q, const void* K_pages, const void* V
                     workspace_bytes, (hipStream_t)stream, &L);
 }
 
+int fqkv_probe_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream) {
+  if (!src) return fail(FQKV_ERR_ARG, "null source pointer");
+  if (bytes == 0 || bytes % 16) return fail(FQKV_ERR_ARG, "bytes: must be a positive multiple of 16, got %zu", bytes);
+  if (!aligned(src, 16)) return fail(FQKV_ERR_ARG, "source must be 16-byte aligned");
+  if (blocks < 1 || blocks > (1 << 20)) return fail(FQKV_ERR_ARG, "blocks: must be in [1, 2^20], got %d", blocks);
+  hipError_t e = launch_stream_read(src, bytes, sink, blocks, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "launch: stream read kernel");
+  return FQKV_OK;
+}
+
 int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, int64_t D,
                     int kv_format, int path, void* stream) {
   if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)

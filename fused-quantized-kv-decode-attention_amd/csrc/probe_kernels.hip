@@ -1,0 +1,49 @@
+// Streaming-read probe: the ceiling the decode kernels are measured against.
+//
+// A decode call at batch 1 reads its KV cache once and writes almost
+// nothing, so the fastest it could possibly run is a kernel that only reads
+// the same number of bytes. stream_read_kernel gives each workgroup one
+// contiguous span of the source (the way the decode kernels give each
+// workgroup one contiguous KV tile) and reads it with 16-byte non-temporal
+// loads, 8 in flight per lane, folding them into one word that is stored
+// only if it equals an impossible value (so the loads cannot be optimised
+// away). bench.py times it on the same number of bytes per call as the
+// headline workload.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "launch.h"
+
+namespace fqkv {
+
+typedef uint32_t p4_t __attribute__((ext_vector_type(4)));
+
+__global__ void __launch_bounds__(256) stream_read_kernel(const p4_t* __restrict__ src, size_t n16, size_t span,
+                                                          uint32_t* sink) {
+  constexpr int U = 8, T = 256;
+  const size_t begin = (size_t)blockIdx.x * span;
+  const size_t end = begin + span < n16 ? begin + span : n16;
+  uint32_t acc = 0;
+  size_t i = begin + threadIdx.x;
+  for (; i + (U - 1) * T < end; i += U * T) {
+    p4_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + i + u * T);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < end; i += T) {
+    const p4_t v = __builtin_nontemporal_load(src + i);
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x9E3779B9u && sink) sink[blockIdx.x] = acc;
+}
+
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, hipStream_t st) {
+  if (!src || bytes % 16 || blocks < 1) return hipErrorInvalidValue;
+  const size_t n16 = bytes / 16, span = (n16 + blocks - 1) / blocks;
+  hipLaunchKernelGGL(stream_read_kernel, dim3(blocks), dim3(256), 0, st, (const p4_t*)src, n16, span, sink);
+  return hipGetLastError();
+}
+
+}  // namespace fqkv

@@ -577,6 +577,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         py::arg("W"), py::arg("CW"));
   m.def("_gqa_sk_fast_timed", &gqa_sk_fast_timed, "gqa_sk_fast with events around the partial kernel");
   m.def("_dequant_kv", &dequant_kv, "dequantise int8/int4 KV through the kernels' conversions");
+  m.def("_probe_stream_read",
+        [](torch::Tensor src, int64_t blocks) {
+          check_gpu({&src});
+          TORCH_CHECK(src.is_contiguous(), "contig: src must be contiguous");
+          const c10::DeviceGuard guard(src.device());
+          check_rc(fqkv_probe_stream_read(src.data_ptr(), (size_t)src.nbytes(), nullptr, (int)blocks, cur_stream(src)),
+                   "launch");
+        },
+        "read a tensor once with streaming loads (the bandwidth ceiling of a decode call)");
   m.def("decode_attn_gqa_int8", &decode_attn_gqa_int8, "GQA-aware int8-KV decode", py::arg("q"), py::arg("K"),
         py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("W"));
   m.def("decode_attn_gqa_int4", &decode_attn_gqa_int4, "GQA-aware int4-KV decode", py::arg("q"), py::arg("K"),

@@ -50,7 +50,7 @@ def _run(cmd, verbose):
 def build_hip_lib(verbose=False):
     """Compile the kernels and the C ABI into libfqkv_decode.so."""
     objs = []
-    for src in ("decode_kernels.hip", "quant_kernels.hip", "capi.cpp"):
+    for src in ("decode_kernels.hip", "quant_kernels.hip", "probe_kernels.hip", "capi.cpp"):
         obj = os.path.join(PKG_DIR, "_obj_" + os.path.splitext(src)[0] + ".o")
         cmd = [HIPCC] + HIP_FLAGS + ["-I", INCLUDE, "-I", CSRC, "-x", "hip",
                                      "-c", os.path.join(CSRC, src), "-o", obj]

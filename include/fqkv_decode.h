@@ -223,6 +223,16 @@ int fqkv_gqa_sk_fast_timed(const void* q, const void* K, const void* V, float* m
                            void* ev_begin, void* ev_end);
 
 /*
+ * Measurement helper: read `bytes` (a multiple of 16) from `src` with
+ * 16-byte streaming loads on `blocks` workgroups of 256 threads and write
+ * nothing unless `sink` (optional, `blocks` words) receives an impossible
+ * checksum. A plain read of the bytes a decode call streams is the
+ * ceiling that call can approach; bench.py reports it beside the headline.
+ * No counterpart in the reference.
+ */
+int fqkv_probe_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream);
+
+/*
  * Dequantise an int8 or int4 KV tensor with the exact device conversion the
  * attention kernels use, writing out[t, d] = (float)q[t, d] * (float)scale[t]
  * for tokens = rows*N token rows. path 0 = the K-side conversion (int -> fp16
