@@ -533,8 +533,21 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
     for (int i = 0; i < F::NKI; ++i) qb[i] = F::qfrag(rQ, qrow * D, i, R);
   }
+  // int8 / int4 scores come out of the matrix cores as 2^-24 (q.k + BIAS
+  // sum(q)) over the query as the operands carry it; qbias = BIAS sum(q) of
+  // the lane's column (zero for fp16)
+  float qbias = 0.0f;
+  if constexpr (F::QUANT) {
+    float qs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < F::NKI; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qs += (float)qb[i][e] * (16777216.0f / F::kunit(e));
+    qbias = F::BIAS * rows4_sum(qs);
+  }
 
   float m_run = -INFINITY, l_run = 0.0f;  // of column n, over the tokens this lane scored
+  float w_run = 0.0f;  // int8 / int4: sum of the lane's PV weights, in acc's units
   int acc_shift = 0;                      // acc holds the true accumulators times 2^acc_shift
   f4_t acc[VE];                           // O^T: step c, reg k = head-dim VE (4R + k) + c of column n
 #pragma unroll
@@ -715,7 +728,10 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) x[g][k] = pick<P>(m1, m2, [&](int j) { return c4[g * P + j][k]; }) * (float)ks[g][k];
+      for (int k = 0; k < 4; ++k) {
+        const float raw = pick<P>(m1, m2, [&](int j) { return c4[g * P + j][k]; });
+        x[g][k] = (F::QUANT ? fmaf(raw, 16777216.0f, -qbias) : raw) * (float)ks[g][k];
+      }
     if (!full) {
 #pragma unroll
       for (int g = 0; g < NG; ++g)
@@ -764,7 +780,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     // p 2^shift = 2^((x - mu) c + shift), the argument as one multiply-add
     const float arg0 = (float)shift - mu * p.c;
     h4_t phi[NG], plo[NG];
-    float psum = 0.0f;
+    float psum = 0.0f, wsum = 0.0f;
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
       float wv[4];
@@ -773,6 +789,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
         const float pw = fast_exp2(fmaf(x[g][k], p.c, arg0));
         psum += pw;
         wv[k] = F::QUANT ? pw * (float)vs[g][k] : pw;
+        if constexpr (F::QUANT) wsum += wv[k];
       }
       // hi through an explicit conversion (round toward zero): converting
       // with a cast lets the compiler fuse the product into a mixed-precision
@@ -789,6 +806,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     }
     const float acc_alpha = F::QUANT ? __builtin_amdgcn_ldexpf(alpha, shift - acc_shift) : alpha;
     l_run = l_run * acc_alpha + psum;
+    if constexpr (F::QUANT) w_run = w_run * acc_alpha + wsum;
     acc_shift = shift;
     // acc needs rescaling only where the maximum or the shift moved and
     // something has been accumulated (acc is all zero while m = -inf)
@@ -807,7 +825,11 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       // operand B of tile t: the weights of the columns that hold tile t
       auto wts = [&](int t, h4_t& bh, h4_t& bl) {
 #pragma unroll
-        for (int dw = 0; dw < VD; ++dw) exchange_4x4(vr[t][0][dw], vr[t][1][dw], vr[t][2][dw], vr[t][3][dw]);
+        for (int dw = 0; dw < VD; ++dw) {
+          exchange_4x4(vr[t][0][dw], vr[t][1][dw], vr[t][2][dw], vr[t][3][dw]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) vr[t][j][dw] = F::vprep(vr[t][j][dw]);
+        }
         bh = phi[t / P];
         bl = plo[t / P];
         if constexpr (P > 1) {
@@ -836,7 +858,15 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   FQKV_STAMP(3);  // last pass's P.V products issued
   // ---- wave totals: l over the four lane rows; O^T rows are disjoint; the
   // P columns of a head add up (same running max and shift in all of them) ----
-  if constexpr (F::QUANT) l_run = __builtin_amdgcn_ldexpf(l_run, -acc_shift);
+  if constexpr (F::QUANT) {
+    // acc[c] * vunit = sum w (v + BIAS): take BIAS sum(w) of the column off
+    const float wb = F::BIAS * rows4_sum(w_run);
+#pragma unroll
+    for (int c = 0; c < VE; ++c)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc[c][k] = fmaf(acc[c][k], F::vunit(c % VG::EPD), -wb);
+    l_run = __builtin_amdgcn_ldexpf(l_run, -acc_shift);
+  }
   l_run = cols_reduce<HG, P, false>(rows4_sum(l_run));
   if constexpr (P > 1) {
 #pragma unroll
@@ -917,7 +947,8 @@ __global__ void __launch_bounds__(64 * NW_MAX) combine_kernel(const float* __res
 }
 
 // Dequantise through the kernels' own conversions (K side: int -> fp16
-// operand; V side: int -> fp32 plus bias), one thread per (token, lane slot).
+// operand, V side: int -> fp16 operand; each times its unit less the bias is
+// the integer), one thread per (token, lane slot).
 template <int FMT, int D>
 __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* __restrict__ Ks,
                                float* __restrict__ out, int64_t tokens, int path) {
@@ -934,7 +965,7 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
     for (int i = 0; i < F::NKI; ++i) {
       const h8_t b = F::kfrag(kr, i);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) out[t * D + F::kd_index(i, kb, e)] = (float)b[e] * sc;
+      for (int e = 0; e < 8; ++e) out[t * D + F::kd_index(i, kb, e)] = ((float)b[e] * F::kunit(e) - F::BIAS) * sc;
     }
   } else {
     using VG = VGeom<F::ROWB, D>;
@@ -945,9 +976,11 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
     load_vchunk<VG::VBYTES, VG::VD>(make_rsrc(Kq + t * F::ROWB, F::ROWB), (uint32_t)i * VG::VBYTES, d);
     const float sc = (float)Ks[t];
 #pragma unroll
+    for (int k = 0; k < VG::VD; ++k) d[k] = F::vprep(d[k]);
+#pragma unroll
     for (int c = 0; c < VG::VE; ++c) {
       const h2_t h = F::vpair(d[c / VG::EPD], d[c / VG::EPD], c % VG::EPD);
-      out[t * D + VG::VE * i + c] = (float)h.x * sc;
+      out[t * D + VG::VE * i + c] = ((float)h.x * F::vunit(c % VG::EPD) - F::BIAS) * sc;
     }
   }
 }

@@ -20,12 +20,19 @@
 //     and element c of the four chunks is the lane's operand of PV step c
 //     (VE = D / 16 steps per tile).
 //
-// Exactness: int8 and int4 values become fp16 through the 0x6400 exponent
-// trick (1024 + u is exact in fp16 for 0 <= u < 1024) followed by an exact
-// subtraction (or, for int4 high nibbles held as 1024 + 16 u, an exact fused
-// multiply-add), so the dequantised value (float)q * (float)scale
-// (decode_attn_int8_mw.cu:24,31; decode_attn_int4.cu:21-23,29-31) is
-// reproduced bit for bit by fqkv_dequant_kv, which calls these same helpers.
+// Exactness: an int8 value x or int4 value n enters the matrix cores as the
+// fp16 subnormal (x + 128) * 2^-24 or (n + 8) * 2^-24 (an int4 high nibble,
+// masked in place, as 16 (n + 8) * 2^-24): the biased integer sits in the
+// mantissa under a zero exponent field, one byte permute or one three-input
+// bitwise op per two values and no floating-point instruction. The matrix
+// cores take fp16 subnormal operands as they are (products are exact in
+// fp32), so a score comes out as 2^-24 (q.k + B sum(q)) and an output
+// element as 2^-24 (w.v + B sum(w)) with the format's bias B; the kernel
+// subtracts B sum(q) per score and B sum(w) once at the end. The operand
+// times unit() is the biased integer exactly, which is how fqkv_dequant_kv,
+// calling these same helpers, reproduces the reference's dequantised value
+// (float)q * (float)scale (decode_attn_int8_mw.cu:24,31;
+// decode_attn_int4.cu:21-23,29-31) bit for bit.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -44,41 +51,34 @@ typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
 
 enum KvFormat : int { KV_F16 = 0, KV_I8 = 1, KV_I4 = 2 };
 
-// Bytes {b_lo, b_hi} selected by `sel` from t, each placed under the fp16
-// exponent byte 0x64: the half2 (1024 + b_lo, 1024 + b_hi).
-// v_perm_b32 byte selector: 0-3 pick bytes of the second operand, 4-7 of the first.
-__device__ __forceinline__ h2_t bytes_under_1024(uint32_t t, uint32_t sel) {
-  return __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0x64646464u, t, sel));
-}
-constexpr uint32_t SEL_B01 = 0x04010400u;  // bytes 0,1 of t
-constexpr uint32_t SEL_B23 = 0x04030402u;  // bytes 2,3 of t
+// v_perm_b32 byte selector: 0-3 pick bytes of the second operand, 4-7 of
+// the first, 0x0C gives a zero byte.
+constexpr uint32_t SEL_B01 = 0x0C010C00u;  // bytes 0, 1 of the second operand, each under a zero byte
+constexpr uint32_t SEL_B23 = 0x0C030C02u;  // bytes 2, 3 likewise
 
-// Four int8 in a dword -> two exact half2 (elements 0,1 and 2,3).
+// Four int8 in a dword -> two half2 of subnormals (x + 128) * 2^-24
+// (elements 0,1 and 2,3): two's complement x ^ 0x80 = x + 128 in [0, 255],
+// each byte placed under a zero high byte.
 __device__ __forceinline__ void i8x4_to_h2x2(uint32_t w, h2_t& a, h2_t& b) {
-  const uint32_t t = w ^ 0x80808080u;  // two's complement x -> x + 128 in [0, 255]
-  const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
-  a = bytes_under_1024(t, SEL_B01) - off;
-  b = bytes_under_1024(t, SEL_B23) - off;
+  const uint32_t t = w ^ 0x80808080u;
+  a = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0u, t, SEL_B01));
+  b = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(0u, t, SEL_B23));
 }
 
-// Two int4 of a dword -> exact half2, one bitwise op and one packed fp16 op
-// each. The nibbles at bits 0-3 and 16-19 (nib_lo) or 4-7 and 20-23
-// (nib_hi) are masked out and placed, sign bit flipped (n ^ 8 = n + 8 mod
-// 16), under the 0x64 exponent byte: 1024 + (n ^ 8), or 1024 + 16 (n ^ 8)
-// for the high nibbles; x - 1032 and x / 16 - 72 (one fused multiply-add,
-// every intermediate exact) then give n.
+// Two int4 of a dword -> half2 of subnormals, one bitwise op each: the
+// nibbles at bits 0-3 and 16-19 (nib_lo) or 4-7 and 20-23 (nib_hi) are
+// masked out with the sign bit flipped (n ^ 8 = n + 8 in [0, 15]), giving
+// (n + 8) * 2^-24 or 16 (n + 8) * 2^-24.
 __device__ __forceinline__ h2_t nib_lo(uint32_t t) {
-  const h2_t off = {(_Float16)1032.0f, (_Float16)1032.0f};
-  return __builtin_bit_cast(h2_t, (t & 0x000F000Fu) ^ 0x64086408u) - off;
+  return __builtin_bit_cast(h2_t, (t & 0x000F000Fu) ^ 0x00080008u);
 }
 __device__ __forceinline__ h2_t nib_hi(uint32_t t) {
-  const h2_t sc = {(_Float16)0.0625f, (_Float16)0.0625f};
-  const h2_t off = {(_Float16)-72.0f, (_Float16)-72.0f};
-  return __builtin_elementwise_fma(__builtin_bit_cast(h2_t, (t & 0x00F000F0u) ^ 0x64806480u), sc, off);
+  return __builtin_bit_cast(h2_t, (t & 0x00F000F0u) ^ 0x00800080u);
 }
 
 // Eight int4 (one dword, byte k = elements 2k (low nibble) and 2k+1) -> four
-// exact half2 in the order [e0 e4 | e1 e5 | e2 e6 | e3 e7].
+// half2 in the order [e0 e4 | e1 e5 | e2 e6 | e3 e7]: even elements at 2^-24
+// per unit, odd ones at 2^-20.
 __device__ __forceinline__ void i4x8_to_h2x4(uint32_t w, h2_t (&h)[4]) {
   const uint32_t w2 = w >> 8;
   h[0] = nib_lo(w);
@@ -194,6 +194,7 @@ struct Fmt<KV_F16, D> {
   __device__ static h8_t qfrag(rsrc_t rq, uint32_t row_elem, int i, int kb) {
     return __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
   }
+  __device__ static uint32_t vprep(uint32_t x) { return x; }
   // element pos (0, 1) of dwords a and b -> half2 (a_pos, b_pos)
   __device__ static h2_t vpair(uint32_t a, uint32_t b, int pos) {
     return __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(b, a, pos ? 0x07060302u : 0x05040100u));
@@ -209,6 +210,10 @@ struct Fmt<KV_I8, D> {
   static constexpr int NKI = D / 32;
   using KT = u4_t;
   static constexpr int KL = D / 64;
+  // operand value * unit = x + BIAS (every K slot and V element)
+  static constexpr float BIAS = 128.0f;
+  __host__ __device__ static constexpr float kunit(int) { return 16777216.0f; }
+  __host__ __device__ static constexpr float vunit(int) { return 16777216.0f; }
   // Load j, lane group kb reads row bytes [64 j + 16 kb, +16) = two MFMA steps.
   __host__ __device__ static constexpr uint32_t klane(int kb) { return 16 * kb; }
   __device__ static void load_k(rsrc_t r, uint32_t off, KT (&kr)[KL]) {
@@ -228,14 +233,13 @@ struct Fmt<KV_I8, D> {
   __device__ static h8_t qfrag(rsrc_t rq, uint32_t row_elem, int i, int kb) {
     return __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
   }
-  // byte pos of dwords a and b -> exact half2 (a_pos, b_pos): the bytes are
-  // placed in the low byte of each half, x ^ 0x80 = x + 128 is put under the
-  // 0x64 exponent byte (1024 + x + 128) and 1152 is subtracted.
+  // a V dword before vpair: x ^ 0x80 = x + 128 in every byte
+  __device__ static uint32_t vprep(uint32_t x) { return x ^ 0x80808080u; }
+  // byte pos of prepared dwords a and b -> half2 of subnormals (a_pos, b_pos):
+  // each byte placed under a zero high byte
   __device__ static h2_t vpair(uint32_t a, uint32_t b, int pos) {
     const uint32_t sel = 0x0C000C00u | ((uint32_t)(4 + pos) << 16) | (uint32_t)pos;
-    const uint32_t t = __builtin_amdgcn_perm(b, a, sel) ^ 0x64806480u;
-    const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
-    return __builtin_bit_cast(h2_t, t) - off;
+    return __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(b, a, sel));
   }
 };
 
@@ -249,6 +253,11 @@ struct Fmt<KV_I4, D> {
   // one load of ROWB/4 bytes (one dword = 8 elements per MFMA step)
   using KT = typename std::conditional<D == 128, u4_t, u2_t>::type;
   static constexpr int KL = 1;
+  // operand value * unit = n + BIAS: K slots 2, 3, 6, 7 of a step and odd V
+  // elements of a dword (high nibbles) sit 16 times higher
+  static constexpr float BIAS = 8.0f;
+  __host__ __device__ static constexpr float kunit(int e) { return ((e >> 1) & 1) ? 1048576.0f : 16777216.0f; }
+  __host__ __device__ static constexpr float vunit(int pos) { return (pos & 1) ? 1048576.0f : 16777216.0f; }
   // Lane group kb reads row bytes [ROWB/4 * kb, +ROWB/4): four lanes cover a row.
   __host__ __device__ static constexpr uint32_t klane(int kb) { return (ROWB / 4) * kb; }
   __device__ static void load_k(rsrc_t r, uint32_t off, KT (&kr)[KL]) {
@@ -263,13 +272,17 @@ struct Fmt<KV_I4, D> {
   __host__ __device__ static constexpr int kd_index(int i, int kb, int e) {
     return (D / 4) * kb + 8 * i + e / 2 + 4 * (e % 2);
   }
+  // the query elements facing high nibbles are divided by 16 (exact unless
+  // the quotient is an fp16 subnormal), so every product carries 2^-24
   __device__ static h8_t qfrag(rsrc_t rq, uint32_t row_elem, int i, int kb) {
     const h8_t v = __builtin_bit_cast(h8_t, buf_load<16>(rq, 2u * (row_elem + kd_index(i, kb, 0))));
-    return h8_t{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
+    auto q16 = [](_Float16 x) { return (_Float16)((float)x * 0.0625f); };
+    return h8_t{v[0], v[4], q16(v[1]), q16(v[5]), v[2], v[6], q16(v[3]), q16(v[7])};
   }
+  __device__ static uint32_t vprep(uint32_t x) { return x; }
   // nibble pos (element pos; byte pos / 2, low nibble first) of dwords a and
-  // b -> exact half2 (a_pos, b_pos): byte pos / 2 of a and of b go to bytes
-  // 0 and 2, whose low or high nibbles nib_lo / nib_hi convert.
+  // b -> half2 of subnormals (a_pos, b_pos): byte pos / 2 of a and of b go to
+  // bytes 0 and 2, whose low or high nibbles nib_lo / nib_hi convert.
   __device__ static h2_t vpair(uint32_t a, uint32_t b, int pos) {
     const uint32_t byte = (uint32_t)(pos >> 1);
     const uint32_t sel = 0x0C000C00u | ((4u + byte) << 16) | byte;
