@@ -252,7 +252,7 @@ def _frac(nbytes, ms):
     return round(nbytes / ms / 1e6 / PEAK_HBM_GBS, 4)
 
 
-def secondary_results(torch, fq, steps=100, warmup=10):
+def secondary_results(torch, fq, steps=400, warmup=50):
     """The reference's other benchmark shapes, in the driver's line.
 
     * mha_b2048_n4096_d128: fp16 / int8 / int4 MHA at batch*heads 2048,

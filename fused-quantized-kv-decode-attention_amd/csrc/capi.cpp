@@ -597,6 +597,17 @@ int fqkv_probe_stream_read(const void* src, size_t bytes, uint32_t* sink, int bl
   return FQKV_OK;
 }
 
+int fqkv_probe_buffer_range(const void* buf, size_t bytes, int records, uint32_t* out, void* stream) {
+  if (!buf || !out) return fail(FQKV_ERR_ARG, "null pointer");
+  if (!aligned(buf, 16) || !aligned(out, 4)) return fail(FQKV_ERR_ARG, "buffer must be 16-byte aligned");
+  if (records < 16 || records % 16) return fail(FQKV_ERR_ARG, "records: must be a positive multiple of 16, got %d", records);
+  if (bytes < (size_t)records + 64)
+    return fail(FQKV_ERR_ARG, "bytes: the buffer must extend 64 bytes past records (%d), got %zu", records, bytes);
+  hipError_t e = launch_buffer_range(buf, records, out, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "launch: buffer range probe");
+  return FQKV_OK;
+}
+
 int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, int64_t D,
                     int kv_format, int path, void* stream) {
   if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)

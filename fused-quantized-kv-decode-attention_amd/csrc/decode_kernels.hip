@@ -95,18 +95,34 @@ __device__ __forceinline__ void exchange_4x4(uint32_t& a0, uint32_t& a1, uint32_
   swap_rows16(a0, a1);
   swap_rows16(a2, a3);
 }
+// Maxima run on order-preserving integer keys of the fp32 bit patterns: a
+// negative value has its magnitude bits flipped, so signed integer order is
+// float order (-0 < +0; the map is its own inverse). fmaxf of a value that
+// arrives through a lane move compiles to two canonicalising moves and the
+// maximum; v_max_i32 needs neither and takes a DPP operand directly.
+__device__ __forceinline__ int fkey(float x) {
+  const int b = __builtin_bit_cast(int, x);
+  return b ^ ((b >> 31) & 0x7FFFFFFF);
+}
+__device__ __forceinline__ float unkey(int k) { return __builtin_bit_cast(float, k ^ ((k >> 31) & 0x7FFFFFFF)); }
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_mov_dpp(x, CTRL, 0xF, 0xF, true);
+}
+
 // All-reduce over the four lane rows (lanes with equal lane % 16). Combining
 // both outputs of each swap makes the result independent of which operand
 // receives which rows.
-__device__ __forceinline__ float rows4_max(float x) {
-  uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
+__device__ __forceinline__ int rows4_max_key(int k) {
+  uint32_t a = (uint32_t)k, b = a;
   swap_rows32(a, b);
-  x = fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-  a = __builtin_bit_cast(uint32_t, x);
+  k = max((int)a, (int)b);
+  a = (uint32_t)k;
   b = a;
   swap_rows16(a, b);
-  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+  return max((int)a, (int)b);
 }
+__device__ __forceinline__ float rows4_max(float x) { return unkey(rows4_max_key(fkey(x))); }
 __device__ __forceinline__ float rows4_sum(float x) {
   uint32_t a = __builtin_bit_cast(uint32_t, x), b = a;
   swap_rows32(a, b);
@@ -145,11 +161,12 @@ __device__ __forceinline__ float dpp_f(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float wave_max(float x) {
-  x = fmaxf(x, dpp_f<0xB1>(x));
-  x = fmaxf(x, dpp_f<0x4E>(x));
-  x = fmaxf(x, dpp_f<0x141>(x));
-  x = fmaxf(x, dpp_f<0x140>(x));
-  return rows4_max(x);
+  int k = fkey(x);
+  k = max(k, dpp_i<0xB1>(k));
+  k = max(k, dpp_i<0x4E>(k));
+  k = max(k, dpp_i<0x141>(k));
+  k = max(k, dpp_i<0x140>(k));
+  return unkey(rows4_max_key(k));
 }
 __device__ __forceinline__ float wave_sum(float x) {
   x += dpp_f<0xB1>(x);
@@ -162,29 +179,48 @@ __device__ __forceinline__ float wave_sum(float x) {
 // Column packing of the score product. A 16 x 16 score tile has 16 head
 // columns but a work item has only HG query heads, so P = min(U, 16 / HG)
 // tiles of a pass share one column set: column n holds head n % HG of tile
-// n / HG of each group of P tiles. cols_reduce combines the P columns of each
+// n / HG of each group of P tiles. cols_fold combines the P columns of each
 // head within a 16-lane row (DPP quad_perm xor 1 / xor 2, row_ror 4 / 8);
 // columns past P * HG take part only in HG = 2 and must hold a neutral value
 // (or, for a maximum, any value of the same pass).
-template <int HG, int P, bool MAX>
-__device__ __forceinline__ float cols_reduce(float x) {
-  auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+// (Sums on fp32 values, maxima on integer keys.)
+template <int HG, int P, typename T, typename Op, typename Mv>
+__device__ __forceinline__ T cols_fold(T x, Op op, Mv mv) {
   if constexpr (P == 1) {
     return x;
   } else if constexpr (HG == 1) {  // columns 0..3: one quad
-    x = op(x, dpp_f<0xB1>(x));
-    return op(x, dpp_f<0x4E>(x));
+    x = op(x, mv(x, std::integral_constant<int, 0xB1>()));
+    return op(x, mv(x, std::integral_constant<int, 0x4E>()));
   } else if constexpr (HG == 2) {  // columns hh, hh + 2, hh + 4, hh + 6
-    x = op(x, dpp_f<0x4E>(x));
-    x = op(x, dpp_f<0x124>(x));
-    return op(x, dpp_f<0x128>(x));
+    x = op(x, mv(x, std::integral_constant<int, 0x4E>()));
+    x = op(x, mv(x, std::integral_constant<int, 0x124>()));
+    return op(x, mv(x, std::integral_constant<int, 0x128>()));
   } else if constexpr (HG == 4) {  // columns hh + 4 j, j = 0..3
-    x = op(x, dpp_f<0x124>(x));
-    return op(x, dpp_f<0x128>(x));
+    x = op(x, mv(x, std::integral_constant<int, 0x124>()));
+    return op(x, mv(x, std::integral_constant<int, 0x128>()));
   } else {  // HG == 8, P == 2: columns hh, hh + 8
     static_assert(HG == 8 && P == 2, "column packing");
-    return op(x, dpp_f<0x128>(x));
+    return op(x, mv(x, std::integral_constant<int, 0x128>()));
   }
+}
+template <int HG, int P>
+__device__ __forceinline__ float cols_sum(float x) {
+  return cols_fold<HG, P>(
+      x, [](float a, float b) { return a + b; }, [](float v, auto c) { return dpp_f<decltype(c)::value>(v); });
+}
+template <int HG, int P>
+__device__ __forceinline__ int cols_max_key(int k) {
+  return cols_fold<HG, P>(
+      k, [](int a, int b) { return max(a, b); }, [](int v, auto c) { return dpp_i<decltype(c)::value>(v); });
+}
+// Maximum of a head over its P columns and the four lane rows (NONNEG: the
+// values are >= 0, whose bit patterns are their own keys).
+template <int HG, int P, bool NONNEG = false>
+__device__ __forceinline__ float head_max(float x) {
+  if constexpr (NONNEG)
+    return __builtin_bit_cast(float, rows4_max_key(cols_max_key<HG, P>(__builtin_bit_cast(int, x))));
+  else
+    return unkey(rows4_max_key(cols_max_key<HG, P>(fkey(x))));
 }
 
 // f(jl) for the lane's tile index jl < P. The selects are bitwise blends
@@ -513,7 +549,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 
   const int n = lane & 15;  // column of S^T, P^T and O^T; token row of the K operand
   const int R = lane >> 4;  // lane row: K dword group; scores and V of tokens 4R .. 4R+3
-  // Column packing (cols_reduce): column n carries head hh of tile jl of each
+  // Column packing (cols_fold): column n carries head hh of tile jl of each
   // group of P tiles; columns past P * HG carry nothing (scores masked).
   constexpr int P = (16 / HG < U) ? 16 / HG : U;
   constexpr int NG = U / P;  // tile groups per pass
@@ -624,8 +660,8 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   constexpr bool PICK_SC = F::QUANT && PAGED && P > 1;
   // contiguous, 8-byte aligned scale rows: a lane's four scales (tokens 4R ..
   // 4R + 3, a multiple of 4 from lo) are one 8-byte load in passes that lie
-  // wholly before hi (a load straddling the descriptor's end could be dropped
-  // whole)
+  // wholly before hi (past the descriptor's end a load reads zeros dword by
+  // dword, so a dword holding a valid and an invalid scale could lose both)
   const bool vec_sc = F::QUANT && !PAGED && sts == 2u && (lo & 3) == 0 &&
                       ((reinterpret_cast<uintptr_t>(Ksr) | reinterpret_cast<uintptr_t>(Vsr)) & 7u) == 0;
   for (int pb = lo + 16 * w; pb < hi; pb += U * step) {
@@ -742,7 +778,9 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
           x[g][k] = ok ? x[g][k] : -INFINITY;
         }
     }
-    float mx = -INFINITY;
+    // the running maximum is the same in every lane of a head, so it joins
+    // the lane's own maximum before the reduction
+    float mx = m_run;
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
@@ -750,7 +788,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
         if constexpr (P * HG < 16) x[g][k] = live ? x[g][k] : -INFINITY;
         mx = fmaxf(mx, x[g][k]);
       }
-    const float mn = fmaxf(m_run, rows4_max(cols_reduce<HG, P, true>(mx)));
+    const float mn = head_max<HG, P>(mx);
     const float mu = (mn == -INFINITY) ? 0.0f : mn;
     const float alpha = fast_exp2((m_run - mu) * p.c);  // exactly 1 while the maximum holds
     // The PV operand carries each fp32 weight w = p * (V scale) as an fp16
@@ -771,7 +809,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
         for (int k = 0; k < 4; ++k) vmax = fmaxf(vmax, (float)vs[g][k]);
       // over the pass (dead columns hold scales of the pass's last tile)
-      vmax = rows4_max(cols_reduce<HG, P, true>(vmax));
+      vmax = head_max<HG, P, true>(vmax);
       // vmax < 2^e with e from the exponent field (vmax is a normal fp32)
       const int e = vmax > 0.0f ? (int)((__builtin_bit_cast(uint32_t, vmax) >> 23) & 0xFFu) - 126 : 0;
       const int ideal = 14 - e;
@@ -867,12 +905,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       for (int k = 0; k < 4; ++k) acc[c][k] = fmaf(acc[c][k], F::vunit(c % VG::EPD), -wb);
     l_run = __builtin_amdgcn_ldexpf(l_run, -acc_shift);
   }
-  l_run = cols_reduce<HG, P, false>(rows4_sum(l_run));
+  l_run = cols_sum<HG, P>(rows4_sum(l_run));
   if constexpr (P > 1) {
 #pragma unroll
     for (int c = 0; c < VE; ++c)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc[c][k] = cols_reduce<HG, P, false>(acc[c][k]);
+      for (int k = 0; k < 4; ++k) acc[c][k] = cols_sum<HG, P>(acc[c][k]);
   }
   if constexpr (F::QUANT) {
 #pragma unroll

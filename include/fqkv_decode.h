@@ -233,6 +233,17 @@ int fqkv_gqa_sk_fast_timed(const void* q, const void* K, const void* V, float* m
 int fqkv_probe_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, void* stream);
 
 /*
+ * Hardware check: what gfx950's raw buffer loads return past a descriptor's
+ * end. A descriptor over the first `records` bytes (a multiple of 16) of
+ * `buf` (`bytes` >= records + 64 long, so no access leaves it) is read at
+ * offsets past its end carried in the VGPR offset, the SGPR offset and the
+ * immediate field, and with a 16-byte load straddling the end; the nine
+ * dwords read go to `out` (see probe_kernels.hip for the order). The attention
+ * kernels rely on zeros in those cases. No counterpart in the reference.
+ */
+int fqkv_probe_buffer_range(const void* buf, size_t bytes, int records, uint32_t* out, void* stream);
+
+/*
  * Dequantise an int8 or int4 KV tensor with the exact device conversion the
  * attention kernels use, writing out[t, d] = (float)q[t, d] * (float)scale[t]
  * for tokens = rows*N token rows. path 0 = the K-side conversion (int -> fp16

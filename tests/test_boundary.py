@@ -198,3 +198,19 @@ def test_capi_layout_entry_points_reject_bad_args(lib):
     assert "null page table" in _err(lib)
     assert fp(*ok, 1, 32, 8, 0, 4, 16, 64, 128, 0, 4096, 256, 2048, 0, 0, 1, 8, None, 0, None) == 1
     assert _err(lib).startswith("pages:")
+
+
+def test_capi_probes_reject_bad_args(lib):
+    fr = lib.fqkv_probe_buffer_range
+    fr.argtypes = [VP, ctypes.c_size_t, ctypes.c_int, VP, VP]
+    assert fr(4096, 256, 256, 4096, None) == 1  # no room past records
+    assert _err(lib).startswith("bytes:")
+    assert fr(4096, 4096, 100, 4096, None) == 1
+    assert _err(lib).startswith("records:")
+    assert fr(None, 4096, 256, 4096, None) == 1
+    fs = lib.fqkv_probe_stream_read
+    fs.argtypes = [VP, ctypes.c_size_t, VP, ctypes.c_int, VP]
+    assert fs(4096, 100, None, 256, None) == 1
+    assert _err(lib).startswith("bytes:")
+    assert fs(4096, 4096, None, 0, None) == 1
+    assert _err(lib).startswith("blocks:")
