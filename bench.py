@@ -854,6 +854,9 @@ def main():
     ap.add_argument("--sweep", action="store_true", help="tune S/W/CW first (table on stderr)")
     ap.add_argument("--merge", choices=("fused", "two-kernel"), default="fused",
                     help="split merge inside the partial kernel (default) or a separate combine kernel")
+    ap.add_argument("--pv", choices=("mfma", "valu"), default="mfma",
+                    help="P.V on the matrix cores (default) or, for A/B runs, on the vector ALUs "
+                         "(fp16, D 128, 1 or 4 heads per work item)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the secondary keys (MHA B=2048, split-K B=8 N=32K, launch floor)")
@@ -882,6 +885,7 @@ def main():
 
     cus = fq.cu_count()
     fq._ext._set_two_kernel_merge(1 if args.merge == "two-kernel" else 0)
+    fq._ext._set_pv_valu(args.pv == "valu")
     if args.calib_copy_mib:
         n = args.calib_copy_mib << 20
         src = torch.ones(n, dtype=torch.uint8, device="cuda")
@@ -945,7 +949,7 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "gqa_sk_fast fp16 decode, Hq=32, Hkv=8, N=%d, D=128, batch 1" % N,
-            "S": S, "W": W, "CW": CW, "merge": args.merge,
+            "S": S, "W": W, "CW": CW, "merge": args.merge, "pv": args.pv,
             "kv_sets": args.kv_sets,
             "kv_bytes_cycled": args.kv_sets * 4 * HKV * N * D,
             "alg_bytes_per_call": alg_bytes(),

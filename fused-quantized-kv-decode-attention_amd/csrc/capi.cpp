@@ -376,6 +376,11 @@ const char* fqkv_last_error(void) { return g_err; }
 
 const char* fqkv_version(void) { return "fqkv_decode 0.1.0 (gfx950)"; }
 
+int fqkv_set_pv_valu(int enable) {
+  set_pv_valu(enable);
+  return FQKV_OK;
+}
+
 int fqkv_set_two_kernel_merge(int enable) {
   g_force_two_kernel.store(enable ? 1 : 0, std::memory_order_relaxed);
   return FQKV_OK;

@@ -43,6 +43,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "kv_formats.h"
 #include "launch.h"
 
@@ -501,9 +503,16 @@ __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const f
   }
 }
 
-template <int FMT, int D, int HG, bool PAGED>
+// PVV: P.V on the vector ALUs instead of the matrix cores (fp16, contiguous
+// rows only): a measurement variant for comparing the two, selected by
+// fqkv_set_pv_valu. Each wave writes its fp32 weights to its own LDS rows
+// and every lane multiplies the V elements it holds after the row exchange
+// (tokens 4R .. 4R+3, elements VE i .. VE i + VE-1 of each tile) by the
+// weights of those tokens for each of its heads.
+template <int FMT, int D, int HG, bool PAGED, bool PVV = false>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
+  static_assert(!PVV || (FMT == KV_F16 && !PAGED), "P.V on the vector ALUs: fp16, contiguous rows");
   using VG = VGeom<F::ROWB, D>;
   constexpr int U = TILES_PER_PASS;
   constexpr int VE = VG::VE;   // PV steps per tile
@@ -588,6 +597,15 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   f4_t acc[VE];                           // O^T: step c, reg k = head-dim VE (4R + k) + c of column n
 #pragma unroll
   for (int c = 0; c < VE; ++c) acc[c] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  // PVV: head h, element VE n + c, over the lane's tokens 4R .. 4R+3 of every tile
+  float accv[PVV ? HG : 1][PVV ? VE : 1];
+#pragma unroll
+  for (int h = 0; h < (PVV ? HG : 1); ++h)
+#pragma unroll
+    for (int c = 0; c < (PVV ? VE : 1); ++c) accv[h][c] = 0.0f;
+  // PVV: the wave's weights, [tile][token][head] fp32, after its K staging rows
+  float* s_pw = nullptr;
+  if constexpr (PVV) s_pw = reinterpret_cast<float*>(s_kstage + nw * F::KSTAGE) + w * (U * 16 * HG);
 
   // Buffer descriptors end at the split's last token, so rows past it read
   // as zeros (their scores are masked); offsets are 32-bit from the row block.
@@ -829,6 +847,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
         wv[k] = F::QUANT ? pw * (float)vs[g][k] : pw;
         if constexpr (F::QUANT) wsum += wv[k];
       }
+      if constexpr (PVV) {
+        if (live) {
+#pragma unroll
+          for (int k = 0; k < 4; ++k) s_pw[((g * P + jl) * 16 + 4 * R + k) * HG + hh] = wv[k];
+        }
+      }
       // hi through an explicit conversion (round toward zero): converting
       // with a cast lets the compiler fuse the product into a mixed-precision
       // multiply-add for one use and not another, and the two roundings of w
@@ -849,10 +873,46 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     // acc needs rescaling only where the maximum or the shift moved and
     // something has been accumulated (acc is all zero while m = -inf)
     if (__builtin_amdgcn_ballot_w64(acc_alpha != 1.0f && m_run != -INFINITY) != 0) {
+      if constexpr (PVV) {
+        // a lane accumulates every head, so each takes its own head's factor,
+        // from lane h (row 0, column h: head h of the pass's first tile); the
+        // factors are the same in every lane row
 #pragma unroll
-      for (int c = 0; c < VE; ++c) acc[c] *= acc_alpha;
+        for (int h = 0; h < HG; ++h) {
+          const float ah = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, acc_alpha), h));
+#pragma unroll
+          for (int c = 0; c < VE; ++c) accv[h][c] *= ah;
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < VE; ++c) acc[c] *= acc_alpha;
+      }
     }
     m_run = mn;
+    if constexpr (PVV) {
+      // the lane's V after the row exchange: chunk j = token 4R + j, half c of
+      // its dwords = element VE n + c; the weights of that token for every
+      // head are one LDS broadcast read per row
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+#pragma unroll
+        for (int dw = 0; dw < VD; ++dw) exchange_4x4(vr[u][0][dw], vr[u][1][dw], vr[u][2][dw], vr[u][3][dw]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float wt[HG];
+#pragma unroll
+          for (int h = 0; h < HG; ++h) wt[h] = s_pw[(u * 16 + 4 * R + j) * HG + h];
+#pragma unroll
+          for (int c = 0; c < VE; ++c) {
+            const uint32_t d2 = vr[u][j][c / 2];
+            const float v = (float)__builtin_bit_cast(_Float16, (uint16_t)((c % 2) ? (d2 >> 16) : (d2 & 0xFFFFu)));
+#pragma unroll
+            for (int h = 0; h < HG; ++h) accv[h][c] = fmaf(v, wt[h], accv[h][c]);
+          }
+        }
+      }
+      continue;
+    }
     // Two tiles per product: v_mfma_f32_16x16x32_f16 contracts over 32
     // operand slots, lane row R's slots 8R .. 8R+3 taking tokens 4R .. 4R+3
     // of tile u and 8R+4 .. 8R+7 the same tokens of tile u + 1 (half the
@@ -906,7 +966,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     l_run = __builtin_amdgcn_ldexpf(l_run, -acc_shift);
   }
   l_run = cols_sum<HG, P>(rows4_sum(l_run));
-  if constexpr (P > 1) {
+  if constexpr (P > 1 && !PVV) {
 #pragma unroll
     for (int c = 0; c < VE; ++c)
 #pragma unroll
@@ -918,13 +978,33 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
       for (int k = 0; k < 4; ++k) acc[c][k] = __builtin_amdgcn_ldexpf(acc[c][k], -acc_shift);
   }
+  if constexpr (PVV) {
+    // sums over the four lane rows: lane n then holds elements VE n .. VE n + VE-1 of every head
+#pragma unroll
+    for (int h = 0; h < HG; ++h)
+#pragma unroll
+      for (int c = 0; c < VE; ++c) accv[h][c] = rows4_sum(accv[h][c]);
+    if (R == 0) {
+#pragma unroll
+      for (int h = 0; h < HG; ++h) {
+        if (h < hcnt) {
+#pragma unroll
+          for (int c = 0; c < VE; c += 4)
+            *reinterpret_cast<fl4_t*>(&s_o[w][h][VE * n + c]) =
+                fl4_t{accv[h][c], accv[h][c + 1], accv[h][c + 2], accv[h][c + 3]};
+        }
+      }
+    }
+  }
   if (n < HG && n < hcnt) {
+    if constexpr (!PVV) {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float* dst = &s_o[w][n][VE * (4 * R + k)];
+      for (int k = 0; k < 4; ++k) {
+        float* dst = &s_o[w][n][VE * (4 * R + k)];
 #pragma unroll
-      for (int c = 0; c < VE; c += 4)
-        *reinterpret_cast<fl4_t*>(dst + c) = fl4_t{acc[c][k], acc[c + 1][k], acc[c + 2][k], acc[c + 3][k]};
+        for (int c = 0; c < VE; c += 4)
+          *reinterpret_cast<fl4_t*>(dst + c) = fl4_t{acc[c][k], acc[c + 1][k], acc[c + 2][k], acc[c + 3][k]};
+      }
     }
     if (R == 0) {
       s_m[n][w] = m_run;
@@ -1024,10 +1104,20 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
 }
 
 // ------------------------------------------------------------ launchers ----
+static std::atomic<int> g_pv_valu{0};
+void set_pv_valu(int on) { g_pv_valu.store(on ? 1 : 0, std::memory_order_relaxed); }
+
 template <int FMT, int D, int HG>
 static hipError_t launch_partial_t(const PartialParams& p, int nblocks, int nw, hipStream_t st) {
   size_t lds = 0;
   if constexpr (Fmt<FMT, D>::STAGE_K) lds = (size_t)nw * Fmt<FMT, D>::KSTAGE;
+  if constexpr (FMT == KV_F16 && D == 128 && (HG == 1 || HG == 4)) {
+    if (!p.page_table && g_pv_valu.load(std::memory_order_relaxed)) {
+      lds += (size_t)nw * TILES_PER_PASS * 16 * HG * sizeof(float);
+      hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false, true>), dim3(nblocks), dim3(64 * nw), lds, st, p);
+      return hipGetLastError();
+    }
+  }
   if (p.page_table)
     hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, true>), dim3(nblocks), dim3(64 * nw), lds, st, p);
   else

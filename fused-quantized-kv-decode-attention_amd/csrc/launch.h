@@ -108,6 +108,8 @@ hipError_t launch_dequant(int fmt, int D, int path, const void* Kq, const void* 
                           int64_t tokens, hipStream_t st);
 hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, int blocks, hipStream_t st);
 hipError_t launch_buffer_range(const void* buf, int records, uint32_t* out, hipStream_t st);
+// Measurement knob: P.V of fp16, D 128, 1 or 4 heads per group, contiguous rows on the vector ALUs.
+void set_pv_valu(int on);
 hipError_t launch_quantize(int src_f16, int fmt, int D, const void* X, void* Q, void* S, int64_t tokens,
                            hipStream_t st);
 hipError_t launch_quantize_append(int src_f16, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,

@@ -616,6 +616,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("_choose_splits", &choose_splits, "split count the single-block entry points use");
   m.def("_cu_count", &cu_count, "compute units of the current device");
   m.def("_version", []() { return std::string(fqkv_version()); });
+  m.def("_set_pv_valu", [](bool enable) { fqkv_set_pv_valu(enable ? 1 : 0); },
+        "measurement knob: P.V on the vector ALUs (fp16, D 128, 1 or 4 heads per group, contiguous rows)");
   m.def("_set_two_kernel_merge", [](bool enable) { fqkv_set_two_kernel_merge(enable ? 1 : 0); },
         "force the two-kernel split merge (testing / comparison)");
 }

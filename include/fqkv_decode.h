@@ -303,6 +303,17 @@ int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, v
  */
 int fqkv_set_two_kernel_merge(int enable);
 
+/*
+ * Measurement knob: with `enable` nonzero, fp16 calls at D = 128 whose work
+ * items hold 1 or 4 query heads (MHA, and GQA with 4 query heads per KV
+ * head) on contiguous rows compute P.V on the vector ALUs instead of the
+ * matrix cores; everything else in the kernel is unchanged, so timing the
+ * two settings compares the two products. Other calls are not affected.
+ * Process-wide, not synchronised with calls in flight. No counterpart in
+ * the reference. Returns FQKV_OK.
+ */
+int fqkv_set_pv_valu(int enable);
+
 /* Number of compute units of the current device (used by the split heuristic). */
 int fqkv_device_cu_count(int* cu_count);
 
