@@ -399,12 +399,14 @@ def _ref_mha(torch, q, Kf, Vf):
 REF_QUANT_D64_MS = {8: (0.2263, 0.2478, 0.2662), 256: (0.4792, 0.4864, 0.4915), 2048: (2.0951, 1.6814, 1.5585)}
 
 
-def suite_mha_quant(torch, fq, steps, warmup, rows):
+def suite_mha_quant(torch, fq, steps, warmup, rows, shapes=None):
     """fp16 / int8 / int4 MHA decode at B in {8, 256, 2048}, N=4096, W=8, at D=128 and at the
-    reference's own D=64 (its A100 numbers alongside)."""
+    reference's own D=64 (its A100 numbers alongside); shapes: (D, B) pairs to run instead."""
     from fqkv_decode import quant
     N, W = 4096, 8
-    for Dm, B in [(128, b) for b in (8, 256, 2048)] + [(64, b) for b in (8, 256, 2048)]:
+    if shapes is None:
+        shapes = [(128, b) for b in (8, 256, 2048)] + [(64, b) for b in (8, 256, 2048)]
+    for Dm, B in shapes:
         g = torch.Generator(device="cuda").manual_seed(1)
         q = torch.randn(B, Dm, device="cuda", generator=g).half()
         per = {"fp16": 2 * B * N * Dm * 2, "int8": 2 * B * N * Dm + 4 * B * N, "int4": B * N * Dm + 4 * B * N}
@@ -461,12 +463,15 @@ def suite_mha_quant(torch, fq, steps, warmup, rows):
 REF_GQA_N4096_MS = {1: (0.2417, 0.5898), 4: (0.4588, 0.8735), 16: (0.4506, 1.6148)}
 
 
-def suite_gqa(torch, fq, steps, warmup, rows):
+def suite_gqa(torch, fq, steps, warmup, rows, shapes=None):
     """decode_attn_gqa vs repeat_kv + MHA kernel: Hq=32, Hkv=8, D=64, B in {1,4,16}, at N=512
-    and at the reference's own N=4096 (its A100 numbers alongside)."""
+    and at the reference's own N=4096 (its A100 numbers alongside); shapes: (N, B) pairs to run
+    instead."""
     Hq, Hkv, Dg, W = 32, 8, 64, 8
     G = Hq // Hkv
-    for N, B in [(512, b) for b in (1, 4, 16)] + [(4096, b) for b in (1, 4, 16)]:
+    if shapes is None:
+        shapes = [(512, b) for b in (1, 4, 16)] + [(4096, b) for b in (1, 4, 16)]
+    for N, B in shapes:
         g = torch.Generator(device="cuda").manual_seed(2)
         per = 2 * B * Hkv * N * Dg * 2
         ns = _nsets(per)
@@ -723,7 +728,7 @@ def suite_quant(torch, fq, steps, warmup, rows):
     torch.cuda.empty_cache()
 
 
-def suite_llama(torch, fq, rows):
+def suite_llama(torch, fq, rows, full=True):
     """End-to-end decode on a random-init Llama-3.2-1B-shaped model (16 layers, 32/8 heads,
     head_dim 64, hidden 2048, fp16) through transformers, SDPA vs the kernel hook
     (the reference's nb:1037-1123 measurements: generate tok/s at prompt 512 + 128 new
@@ -788,6 +793,12 @@ def suite_llama(torch, fq, rows):
                                              "prompt": 512, "new_tokens": 128}}
     r["sdpa_tok_s"] = round(tok_per_s("sdpa"), 2)
     r["kernel_tok_s"] = round(tok_per_s(name), 2)
+    if not full:  # generate tok/s only (the reference's end_to_end.json)
+        rows.append(r)
+        set_impl("sdpa")
+        del model
+        torch.cuda.empty_cache()
+        return
     for ctx in (512, 2048, 8192):
         r["decode_ms_sdpa_ctx%d" % ctx] = round(decode_ms("sdpa", ctx), 4)
         r["decode_ms_kernel_ctx%d" % ctx] = round(decode_ms(name, ctx), 4)
@@ -813,6 +824,60 @@ def suite_llama(torch, fq, rows):
 
 
 SUITES = ("mha_small", "mha_quant", "gqa", "splitk", "splitk_quant", "paged", "quant", "llama")
+
+
+# The reference's end-to-end result (benchmarks/end_to_end.json): Llama-3.2-1B, prompt 512,
+# 128 new tokens, SDPA vs its kernel hook, on its A100.
+REF_E2E_TOK_S = (51.887, 54.680)
+
+
+def reference_tables(torch, fq):
+    """The reference's other published tables at their own shapes, for the default line:
+    * standalone_quant_d64 (benchmarks/standalone_quant.json): fp16 / int8 / int4 MHA at
+      B in {8, 256, 2048}, N 4096, D 64, W 8, with the int8 / int4 speed-ups over fp16;
+    * gqa_aware_n4096_d64 (benchmarks/gqa_aware.json): decode_attn_gqa vs repeat_kv + the
+      MHA kernel at Hq 32 / Hkv 8, N 4096, D 64, B in {1, 4, 16};
+    * end_to_end_llama (benchmarks/end_to_end.json): generate tok/s at prompt 512 + 128 new
+      tokens on a random-init Llama-3.2-1B-shaped model, SDPA vs the kernel hook (best of 3).
+    Each row is gated against fp32 PyTorch on the GPU (max-abs <= 2e-3), loop-timed like the
+    suite (400 calls after 40 warm-ups); the reference's A100 numbers ride along."""
+    rows = []
+    suite_mha_quant(torch, fq, 400, 40, rows, shapes=[(64, b) for b in (8, 256, 2048)])
+    sq = {}
+    for r in rows:
+        fmt, B = r["bench"].split("_")[1], r["config"]["B"]
+        if r["max_abs_err_vs_fp32"] > 2e-3:
+            raise RuntimeError("reference-table gate failed: %s B=%d max-abs %.3e" % (fmt, B, r["max_abs_err_vs_fp32"]))
+        e = sq.setdefault("B%d" % B, {"gate_max_abs_err": 0.0, "ref_a100_us": {}})
+        e[fmt + "_us"] = r["us_per_call"]
+        e[fmt + "_frac"] = r["frac_of_8TBps"]
+        e["ref_a100_us"][fmt] = round(r["ref_a100_us"], 2)
+        e["gate_max_abs_err"] = max(e["gate_max_abs_err"], r["max_abs_err_vs_fp32"])
+    for e in sq.values():
+        e["int8_speedup_vs_fp16"] = round(e["fp16_us"] / e["int8_us"], 3)
+        e["int4_speedup_vs_fp16"] = round(e["fp16_us"] / e["int4_us"], 3)
+    rows = []
+    suite_gqa(torch, fq, 400, 40, rows, shapes=[(4096, b) for b in (1, 4, 16)])
+    ga = {}
+    for r in rows:
+        if r["max_abs_err_vs_fp32"] > 2e-3:
+            raise RuntimeError("reference-table gate failed: gqa B=%d" % r["config"]["B"])
+        ga["B%d" % r["config"]["B"]] = {
+            "gqa_us": r["us_per_call"], "repeat_kv_mha_us": r["expand_mha_us"], "speedup": r["speedup_vs_expand"],
+            "ref_a100_gqa_us": round(r["ref_a100_gqa_us"], 1), "ref_a100_repeat_kv_us": round(r["ref_a100_expand_us"], 1),
+            "gate_max_abs_err": r["max_abs_err_vs_fp32"]}
+    out = {"standalone_quant_d64": sq, "gqa_aware_n4096_d64": ga}
+    rows = []
+    try:
+        suite_llama(torch, fq, rows, full=False)
+        r = rows[0]
+        out["end_to_end_llama"] = {"sdpa_tok_s": r["sdpa_tok_s"], "kernel_tok_s": r["kernel_tok_s"],
+                                   "speedup": round(r["kernel_tok_s"] / r["sdpa_tok_s"], 3),
+                                   "model": r["config"]["model"], "prompt": 512, "new_tokens": 128,
+                                   "ref_a100_tok_s": {"sdpa": REF_E2E_TOK_S[0], "kernel": REF_E2E_TOK_S[1]}}
+    except ImportError as e:  # transformers absent: the row is skipped, not faked
+        out["end_to_end_llama"] = {"skipped": str(e)}
+    return out
 
 
 def run_suite(torch, fq, path, steps=400, warmup=40, only=SUITES):
@@ -982,6 +1047,7 @@ def main():
         % (ceil["blocks"], ceil["us_per_call"], ceil["GBps"], 100 * ceil["headline_frac_of_ceiling"]))
     if not args.no_secondary:
         line.update(secondary_results(torch, fq))
+        line["reference_tables"] = reference_tables(torch, fq)
     if args.suite:
         run_suite(torch, fq, args.suite, only=only)
     if not args.no_cpu_baseline:
