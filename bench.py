@@ -521,8 +521,8 @@ def suite_splitk(torch, fq, steps, warmup, rows):
         ref = _ref_mha(torch, q, K0.float().repeat_interleave(G, 0), V0.float().repeat_interleave(G, 0))
         nbytes = B * (4 * Hkv * N * Dd + 4 * Hq * Dd)
         best = None
-        for S in (8, 16, 32, 64, 128):
-            if S > N // 16:
+        for S in (1, 2, 4, 8, 16, 32, 64, 128):
+            if S > max(1, N // 16):
                 continue
             for W in (4, 8):
                 mp = torch.empty(B * Hq, S, device="cuda")
