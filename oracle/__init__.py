@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY. Only ``tests/``, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of ``bench.py`` may import this package, and only as the
-checker or as the timed CPU baseline. The product (the HIP library and its
+checker (the CPU baseline times the reference's own PyTorch expression and
+checks its result here). The product (the HIP library and its
 PyTorch binding) never imports, links or calls anything here, and has no CPU
 fallback: it fails loudly when its HIP extension is missing.
 
