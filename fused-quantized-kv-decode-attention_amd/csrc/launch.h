@@ -73,6 +73,14 @@ struct PartialParams {
   int split_major;  // blockIdx.x = s * nwsg + wsg (else wsg * S + s)
   int blk_d;        // the divisor of that decomposition: nwsg or S
   FastDiv div_blk, div_groups, div_hkv;
+  // Head grouping (hg_k = 0: off): in a token-major layout the rows of 2^hg_k
+  // neighbouring KV heads share each 128-byte line of a token (two 64-byte
+  // int4 rows at D 128). Group wsg is then renumbered so those heads' work
+  // items lie 2^hg_d apart in group order, which the round-robin dealing of
+  // workgroups to the 8 XCDs puts on one XCD at about the same time: all but
+  // the first read the span from that XCD's L2. Only the order of work
+  // changes, so results do not depend on where workgroups run.
+  int hg_k, hg_d;   // log2 heads per span, log2 distance between them in group order
 };
 
 // The reference's contiguous layout: K, V [rows, N, row_bytes], scales [rows, N].
