@@ -477,6 +477,8 @@ int fqkv_gqa_sk_fast_noalloc(const void* q, const void* K, const void* V, void* 
   if (S < 1 || S > (1 << 20)) return fail(FQKV_ERR_ARG, "S: split count must be in [1, 2^20], got %lld", (long long)S);
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
     return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
+  if (Hq > (int64_t(1) << 24))  // keeps the size arithmetic below far from overflow
+    return fail(FQKV_ERR_ARG, "heads: Hq (%lld) too large for the no-allocation scratch", (long long)Hq);
   // m [Hq*S], l [Hq*S], then acc [Hq*S*D] from a 16-byte boundary
   const size_t acc_off = (size_t)((2 * Hq * S + 3) & ~(int64_t)3) * sizeof(float);
   const size_t need = acc_off + (size_t)Hq * (size_t)S * (size_t)D * sizeof(float);

@@ -214,3 +214,17 @@ def test_capi_probes_reject_bad_args(lib):
     assert _err(lib).startswith("bytes:")
     assert fs(4096, 4096, None, 0, None) == 1
     assert _err(lib).startswith("blocks:")
+
+
+def test_capi_noalloc_rejects_before_any_hip_call(lib):
+    f = lib.fqkv_gqa_sk_fast_noalloc
+    f.argtypes = [VP] * 4 + [I64] * 7 + [VP]
+    p = 4096  # aligned, never dereferenced: every check below fails before a HIP call
+    assert f(p, p, p, p, 1 << 30, 8, 1024, 128, 4, 8, 8, None) == 1
+    assert _err(lib).startswith("heads:")
+    assert f(p, p, p, p, 256, 8, 1024, 128, 64, 8, 8, None) == 1  # 8.4 MB of partials > 8 MiB
+    assert _err(lib).startswith("S:")
+    assert f(p, p, p, p, 32, 8, 1024, 128, 0, 8, 8, None) == 1
+    assert _err(lib).startswith("S:")
+    assert f(p, p, p, p, 30, 8, 1024, 128, 4, 8, 8, None) == 1
+    assert _err(lib).startswith("heads:")
