@@ -56,6 +56,26 @@ def test_nhd_quantized(fmt):
     assert maxerr(out, ref) <= TOL
 
 
+@pytest.mark.parametrize("B", [8, 2])
+def test_nhd_int4_head_grouping_equals_contiguous(B):
+    """Token-major int4 rows are 64 bytes, so KV heads h and h ^ 1 share each 128-byte line
+    and the launcher renumbers the work items to put such heads on one XCD. At B 8 (64 rows,
+    4 splits, groups interleaved with their splits) and B 2 (16 rows, 16 splits, split-major
+    order) the renumbering is not the identity; it changes only which workgroup computes what,
+    so the output must equal the contiguous layout's bit for bit, and the oracle."""
+    g = torch.Generator().manual_seed(52 + B)
+    Hq, Hkv, N, D = 32, 8, 2000, 128
+    q = draw(g, B, Hq, D).half()
+    Kq, Ks, Kf = quantize("int4", draw(g, B, N, Hkv, D))
+    Vq, Vs, Vf = quantize("int4", draw(g, B, N, Hkv, D))
+    out = fq.decode_attn_gqa_nhd(q.cuda(), Kq, Vq, 8, Ks, Vs)
+    hm = lambda t: t.transpose(1, 2).contiguous()  # [B, N, Hkv, ...] -> [B, Hkv, N, ...]
+    ref_c = fq.decode_attn_gqa_int4(q.cuda(), hm(Kq), hm(Vq), hm(Ks), hm(Vs), 8)
+    assert torch.equal(out, ref_c)
+    ref = oracle.gqa_attention(q.numpy(), Kf.transpose(0, 2, 1, 3), Vf.transpose(0, 2, 1, 3))
+    assert maxerr(out, ref) <= TOL
+
+
 def paged_cache(g, lens, Hkv, D, page, fmt, hnd=False, spare=3):
     """Scatter per-sequence K/V into pages at shuffled page ids; returns the
     device pages (NHD views), page table, lengths and the float64 per-sequence caches."""
