@@ -703,17 +703,19 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       if constexpr (F::STAGE_K)
-        F::load_k_rows(src[u].k, src[u].off + koff, ts, kr[u]);
+        F::load_k_rows(src[u].k, koff + (F::SOFF_TILE ? 0u : src[u].off), ts, kr[u], F::SOFF_TILE ? src[u].off : 0u);
       else
-        F::load_k(src[u].k, src[u].off + koff, kr[u]);
+        F::load_k(src[u].k, koff + (F::SOFF_TILE ? 0u : src[u].off), kr[u], F::SOFF_TILE ? src[u].off : 0u);
     }
     if constexpr (F::QUANT) {
       if constexpr (!PAGED) {
         if (vec_sc && full) {
 #pragma unroll
           for (int g = 0; g < NG; ++g) {
-            const uint32_t so = (uint32_t)(pb + g * P * step + lane_tok) * 2u;
-            const u2_t a = buf_load<8>(rKs, so), c = buf_load<8>(rVs, so);
+            const uint32_t so = (uint32_t)(pb + g * P * step) * 2u;  // wave-uniform
+            const uint32_t vo = (uint32_t)lane_tok * 2u + (F::SOFF_TILE ? 0u : so);
+            const u2_t a = buf_load<8>(rKs, vo, F::SOFF_TILE ? so : 0u);
+            const u2_t c = buf_load<8>(rVs, vo, F::SOFF_TILE ? so : 0u);
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
               ks[g][k] = __builtin_bit_cast(_Float16, (uint16_t)(a[k / 2] >> (16 * (k % 2))));
@@ -723,11 +725,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
         } else {
 #pragma unroll
           for (int g = 0; g < NG; ++g) {
-            const uint32_t so = (uint32_t)(pb + g * P * step + lane_tok) * sts;
+            const uint32_t so = (uint32_t)(pb + g * P * step) * sts;  // wave-uniform
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              ks[g][k] = __builtin_bit_cast(_Float16, buf_load<2>(rKs, so + (uint32_t)k * sts));
-              vs[g][k] = __builtin_bit_cast(_Float16, buf_load<2>(rVs, so + (uint32_t)k * sts));
+              const uint32_t vo = (uint32_t)(lane_tok + k) * sts + (F::SOFF_TILE ? 0u : so);
+              ks[g][k] = __builtin_bit_cast(_Float16, buf_load<2>(rKs, vo, F::SOFF_TILE ? so : 0u));
+              vs[g][k] = __builtin_bit_cast(_Float16, buf_load<2>(rVs, vo, F::SOFF_TILE ? so : 0u));
             }
           }
         }
@@ -757,9 +760,10 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const uint32_t base = src[u].off + voff;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) load_vchunk<VG::VBYTES, VD>(src[u].v, base + (uint32_t)(4 * j) * ts, vr[u][j]);
+      for (int j = 0; j < 4; ++j)
+        load_vchunk<VG::VBYTES, VD>(src[u].v, voff + (uint32_t)(4 * j) * ts + (F::SOFF_TILE ? 0u : src[u].off),
+                                    vr[u][j], F::SOFF_TILE ? src[u].off : 0u);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
 
