@@ -191,9 +191,14 @@ template <int HG, int P, typename T, typename Op, typename Mv>
 __device__ __forceinline__ T cols_fold(T x, Op op, Mv mv) {
   if constexpr (P == 1) {
     return x;
-  } else if constexpr (HG == 1) {  // columns 0..3: one quad
+  } else if constexpr (HG == 1 && P <= 4) {  // columns 0..3: one quad
     x = op(x, mv(x, std::integral_constant<int, 0xB1>()));
     return op(x, mv(x, std::integral_constant<int, 0x4E>()));
+  } else if constexpr (HG == 1) {  // columns 0..P-1: the whole row
+    x = op(x, mv(x, std::integral_constant<int, 0xB1>()));
+    x = op(x, mv(x, std::integral_constant<int, 0x4E>()));
+    x = op(x, mv(x, std::integral_constant<int, 0x124>()));
+    return op(x, mv(x, std::integral_constant<int, 0x128>()));
   } else if constexpr (HG == 2) {  // columns hh, hh + 2, hh + 4, hh + 6
     x = op(x, mv(x, std::integral_constant<int, 0x4E>()));
     x = op(x, mv(x, std::integral_constant<int, 0x124>()));
@@ -227,24 +232,23 @@ __device__ __forceinline__ float head_max(float x) {
 }
 
 // f(jl) for the lane's tile index jl < P. The selects are bitwise blends
-// under the loop-invariant lane masks m1 = -(jl & 1), m2 = -((jl >> 1) & 1)
-// (one v_bfi_b32 each): written as conditionals, the compiler turns the
-// chain into a per-lane indexed array in scratch memory.
+// under the loop-invariant lane masks m[i] = -((jl >> i) & 1) (one bitwise
+// select each, P - 1 per pick): written as conditionals, the compiler turns
+// the chain into a per-lane indexed array in scratch memory.
 template <typename T>
 __device__ __forceinline__ T blend(uint32_t m, T a, T b) {  // m ? b : a
   static_assert(sizeof(T) == 4, "32-bit values");
   const uint32_t x = __builtin_bit_cast(uint32_t, a), y = __builtin_bit_cast(uint32_t, b);
   return __builtin_bit_cast(T, (x & ~m) | (y & m));
 }
-template <int P, typename Fn>
-__device__ __forceinline__ auto pick(uint32_t m1, uint32_t m2, Fn f) {
+template <int P, int J0 = 0, typename Fn>
+__device__ __forceinline__ auto pick(const uint32_t (&m)[4], Fn f) {
+  static_assert(P == 1 || P == 2 || P == 4 || P == 8 || P == 16, "column packing");
   if constexpr (P == 1) {
-    return f(0);
-  } else if constexpr (P == 2) {
-    return blend(m1, f(0), f(1));
+    return f(J0);
   } else {
-    static_assert(P == 4, "column packing");
-    return blend(m2, blend(m1, f(0), f(1)), blend(m1, f(2), f(3)));
+    constexpr int B = P == 2 ? 0 : (P == 4 ? 1 : (P == 8 ? 2 : 3));  // the bit that halves [J0, J0 + P)
+    return blend(m[B], pick<P / 2, J0>(m, f), pick<P / 2, J0 + P / 2>(m, f));
   }
 }
 
@@ -510,12 +514,26 @@ __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const f
 // and every lane multiplies the V elements it holds after the row exchange
 // (tokens 4R .. 4R+3, elements VE i .. VE i + VE-1 of each tile) by the
 // weights of those tokens for each of its heads.
+// 16-token tiles a wave loads per pass (one online-softmax step per pass).
+// With one query head per work item, column packing gives each tile of the
+// pass its own score column, so a pass of U tiles keeps U of the 16 columns
+// busy and the softmax instructions of a pass are shared by U tiles. Eight
+// tiles pay off for contiguous int4 at D 64, whose 32-byte rows leave the
+// registers for them (124 VGPRs, 4 waves per SIMD): MHA B 2048, N 4096
+// 100.6 -> 95.7 us, B 256 19.2 -> 17.4 us. Measured slower, and kept at four:
+// int4 at D 128 (B 256 +14 %), int8 at D 64 (B 256 +12 %), sixteen tiles for
+// int4 (B 2048 +8 % at D 64; 2 waves per SIMD), and the paged rows (2 waves).
+template <int FMT, int D, int HG, bool PAGED, bool PVV>
+constexpr int tiles_per_pass() {
+  return (FMT == KV_I4 && D == 64 && HG == 1 && !PAGED && !PVV) ? 8 : 4;
+}
+
 template <int FMT, int D, int HG, bool PAGED, bool PVV = false>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
   static_assert(!PVV || (FMT == KV_F16 && !PAGED), "P.V on the vector ALUs: fp16, contiguous rows");
   using VG = VGeom<F::ROWB, D>;
-  constexpr int U = TILES_PER_PASS;
+  constexpr int U = tiles_per_pass<FMT, D, HG, PAGED, PVV>();
   constexpr int VE = VG::VE;   // PV steps per tile
   constexpr int VD = VG::VD;   // dwords per V chunk
   __shared__ float s_o[NW_MAX][HG][opitch<D>()];
@@ -573,7 +591,8 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   const bool live = n < P * HG;
   const int jl = live ? n / HG : P - 1;
   const int hh = n % HG;
-  const uint32_t m1 = (jl & 1) ? ~0u : 0u, m2 = (jl & 2) ? ~0u : 0u;  // pick() masks
+  const uint32_t jm[4] = {(jl & 1) ? ~0u : 0u, (jl & 2) ? ~0u : 0u, (jl & 4) ? ~0u : 0u,
+                          (jl & 8) ? ~0u : 0u};  // pick() masks
 
   // Query operand B of the score product: lane l holds head hh, elements
   // kd_index(i, R, 0..7). The descriptor covers only this group's hcnt query
@@ -773,8 +792,8 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           auto bits = [](_Float16 v) { return (uint32_t)__builtin_bit_cast(uint16_t, v); };
-          ks[g][k] = __builtin_bit_cast(_Float16, (uint16_t)pick<P>(m1, m2, [&](int j) { return bits(kt[g * P + j][k]); }));
-          vs[g][k] = __builtin_bit_cast(_Float16, (uint16_t)pick<P>(m1, m2, [&](int j) { return bits(vt[g * P + j][k]); }));
+          ks[g][k] = __builtin_bit_cast(_Float16, (uint16_t)pick<P>(jm, [&](int j) { return bits(kt[g * P + j][k]); }));
+          vs[g][k] = __builtin_bit_cast(_Float16, (uint16_t)pick<P>(jm, [&](int j) { return bits(vt[g * P + j][k]); }));
         }
     }
 
@@ -795,7 +814,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     for (int g = 0; g < NG; ++g)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const float raw = pick<P>(m1, m2, [&](int j) { return c4[g * P + j][k]; });
+        const float raw = pick<P>(jm, [&](int j) { return c4[g * P + j][k]; });
         x[g][k] = (F::QUANT ? fmaf(raw, 16777216.0f, -qbias) : raw) * (float)ks[g][k];
       }
     if (!full) {
@@ -804,7 +823,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
           bool ok = pb + g * P * step + lane_tok + k < hi;
-          if constexpr (PAGED) ok = ok && pick<P>(m1, m2, [&](int j) { return src[g * P + j].ok ? ~0u : 0u; }) != 0u;
+          if constexpr (PAGED) ok = ok && pick<P>(jm, [&](int j) { return src[g * P + j].ok ? ~0u : 0u; }) != 0u;
           x[g][k] = ok ? x[g][k] : -INFINITY;
         }
     }
@@ -1121,11 +1140,22 @@ void set_pv_valu(int on) { g_pv_valu.store(on ? 1 : 0, std::memory_order_relaxed
 
 template <int FMT, int D, int HG>
 static hipError_t launch_partial_t(const PartialParams& p, int nblocks, int nw, hipStream_t st) {
+  // nw is a maximum: a split shorter than one pass of nw waves would leave
+  // waves with nothing to load, so take the fewest waves (at least 2) that
+  // still cover the split in one pass -- but, when the splits are merged in
+  // the kernel, no fewer than the merge has (head, 64-dim block) units, so
+  // that every unit keeps a wave of its own.
+  {
+    const int u = p.page_table ? tiles_per_pass<FMT, D, HG, true, false>() : tiles_per_pass<FMT, D, HG, false, false>();
+    const int tiles = (p.chunk + 15) / 16;
+    const int units = p.S > 1 ? HG * (D / 64) : 1;
+    while (nw > 2 && nw / 2 >= units && (nw / 2) * u >= tiles) nw /= 2;
+  }
   size_t lds = 0;
   if constexpr (Fmt<FMT, D>::STAGE_K) lds = (size_t)nw * Fmt<FMT, D>::KSTAGE;
   if constexpr (FMT == KV_F16 && D == 128 && (HG == 1 || HG == 4)) {
     if (!p.page_table && g_pv_valu.load(std::memory_order_relaxed)) {
-      lds += (size_t)nw * TILES_PER_PASS * 16 * HG * sizeof(float);
+      lds += (size_t)nw * tiles_per_pass<FMT, D, HG, false, true>() * 16 * HG * sizeof(float);
       hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false, true>), dim3(nblocks), dim3(64 * nw), lds, st, p);
       return hipGetLastError();
     }
@@ -1154,14 +1184,6 @@ hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, i
   if ((nw != 2 && nw != 4 && nw != 8) || nblocks < 1 || params.S < 1 || params.ngroups < 1 || params.hkv < 1 ||
       nblocks % params.S != 0)
     return hipErrorInvalidValue;
-  // nw is a maximum: a split shorter than one pass of nw waves would leave
-  // waves with nothing to load, so take the fewest waves (at least 2) that
-  // still cover the split in one pass -- but, when the splits are merged in
-  // the kernel, no fewer than the merge has (head, 64-dim block) units, so
-  // that every unit keeps a wave of its own.
-  const int tiles = (params.chunk + 15) / 16;
-  const int units = params.S > 1 ? hg * (D / 64) : 1;
-  while (nw > 2 && nw / 2 >= units && (nw / 2) * TILES_PER_PASS >= tiles) nw /= 2;
   PartialParams p = params;
   p.split_major = p.S >= 16;
   p.blk_d = p.split_major ? nblocks / p.S : p.S;

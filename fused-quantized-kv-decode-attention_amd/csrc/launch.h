@@ -99,10 +99,6 @@ inline void set_contiguous_layout(PartialParams& p, int64_t rows, int64_t N, int
   p.num_pages = 0;
 }
 
-// 16-token tiles each wave of the partial kernel loads per pass (one online-
-// softmax step per pass).
-constexpr int TILES_PER_PASS = 4;
-
 // In-kernel split merge: each call with S > 1 takes one of SPLIT_SLOTS slots
 // of MAX_SPLIT_GROUPS arrival counters (one per (KV row, head group)).
 constexpr int SPLIT_SLOTS = 16;

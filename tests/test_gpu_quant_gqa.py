@@ -88,6 +88,43 @@ def test_gqa_sk_fast_quantized(fmt, Hq, Hkv, N, D, S, W, merge_mode):
     np.testing.assert_allclose(op.cpu().numpy(), acc, rtol=1e-4, atol=2e-4)
 
 
+@pytest.mark.parametrize("N", [1, 17, 100, 127, 128, 129, 255, 257, 383, 1000])
+@pytest.mark.parametrize("W", [2, 4, 8])
+def test_int4_d64_single_head_ragged_passes(N, W):
+    """int4 at D = 64 with one query head per work item loads 8 tiles (128 tokens)
+    per wave pass: token counts on both sides of a pass and of a whole round of
+    waves, against the oracle."""
+    g = torch.Generator().manual_seed(43 + N)
+    B, D = 3, 64
+    q = draw(g, B, D).half()
+    Kq, Ks, Kf = quantized("int4", draw(g, B, N, D))
+    Vq, Vs, Vf = quantized("int4", draw(g, B, N, D))
+    out = fq.decode_attn_int4(q.cuda(), Kq, Vq, Ks, Vs, W)
+    assert maxerr(out, oracle.attention(q.numpy(), Kf, Vf)) <= TOL
+
+
+@pytest.mark.parametrize("N,S,W", [(100, 3, 8), (257, 2, 4), (1000, 7, 8), (4095, 16, 8), (129, 1, 2),
+                                   (2048, 32, 4)])
+def test_int4_d64_single_head_split_k_ragged(N, S, W, merge_mode):
+    """Split-K over int4 at D = 64 with one query head per KV head (8-tile passes):
+    splits that end inside a pass, output and scratch against the oracle."""
+    g = torch.Generator().manual_seed(47 + N)
+    H, D = 4, 64
+    q = draw(g, H, D).half()
+    Kq, Ks, Kf = quantized("int4", draw(g, H, N, D))
+    Vq, Vs, Vf = quantized("int4", draw(g, H, N, D))
+    mp = torch.empty(H, S, device="cuda")
+    lp = torch.empty(H, S, device="cuda")
+    op = torch.empty(H, S, D, device="cuda")
+    o = torch.empty(H, D, device="cuda", dtype=torch.float16)
+    fq.gqa_sk_fast_int4(q.cuda(), Kq, Vq, Ks, Vs, mp, lp, op, o, S, W, 8)
+    assert maxerr(o, oracle.gqa_attention(q.numpy()[None], Kf[None], Vf[None])[0]) <= TOL
+    m, l, acc = oracle.split_partials(q.numpy(), Kf, Vf, S)
+    assert np.array_equal(np.isneginf(mp.cpu().numpy()), np.isneginf(m))
+    np.testing.assert_allclose(lp.cpu().numpy(), l, rtol=1e-4, atol=1e-5)
+    np.testing.assert_allclose(op.cpu().numpy(), acc, rtol=1e-4, atol=2e-4)
+
+
 def test_gqa_quantized_matches_mha_kernel_on_expanded_cache():
     """GQA int8 = the reference-style MHA int8 kernel on repeat_kv-expanded K/V and scales."""
     g = torch.Generator().manual_seed(42)
