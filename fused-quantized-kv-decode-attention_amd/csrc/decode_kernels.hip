@@ -241,6 +241,36 @@ __device__ __forceinline__ T blend(uint32_t m, T a, T b) {  // m ? b : a
   const uint32_t x = __builtin_bit_cast(uint32_t, a), y = __builtin_bit_cast(uint32_t, b);
   return __builtin_bit_cast(T, (x & ~m) | (y & m));
 }
+// Lane n of each 16-lane row takes lane n + sh of the row (0 past its end):
+// DPP row_shl, sh a compile-time constant once the caller's loop is unrolled.
+template <int SH>
+__device__ __forceinline__ uint32_t row_shl_c(uint32_t x) {
+  if constexpr (SH == 0)
+    return x;
+  else
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x100 + SH, 0xF, 0xF, true);
+}
+__device__ __forceinline__ uint32_t row_shl(uint32_t x, int sh) {
+  switch (sh) {
+    case 1: return row_shl_c<1>(x);
+    case 2: return row_shl_c<2>(x);
+    case 3: return row_shl_c<3>(x);
+    case 4: return row_shl_c<4>(x);
+    case 5: return row_shl_c<5>(x);
+    case 6: return row_shl_c<6>(x);
+    case 7: return row_shl_c<7>(x);
+    case 8: return row_shl_c<8>(x);
+    case 9: return row_shl_c<9>(x);
+    case 10: return row_shl_c<10>(x);
+    case 11: return row_shl_c<11>(x);
+    case 12: return row_shl_c<12>(x);
+    case 13: return row_shl_c<13>(x);
+    case 14: return row_shl_c<14>(x);
+    case 15: return row_shl_c<15>(x);
+    default: return x;
+  }
+}
+
 template <int P, int J0 = 0, typename Fn>
 __device__ __forceinline__ auto pick(const uint32_t (&m)[4], Fn f) {
   static_assert(P == 1 || P == 2 || P == 4 || P == 8 || P == 16, "column packing");
@@ -952,6 +982,13 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
     for (int u = 0; u < U; u += 2) {
       // operand B of tile t: the weights of the columns that hold tile t
+      // (HG (t % P) .. + HG - 1). fp16 moves them down the row to columns
+      // 0 .. HG - 1, so every tile of every pass accumulates into the HG
+      // columns of O^T that are emitted and no column sum is left for the
+      // end (the other columns gather weights of other tiles, never read).
+      // int8 / int4 keep them in place, zero elsewhere: their products carry
+      // the bias B sum(w) until the end, and one column holding P tiles'
+      // biased sums measured a few 1e-4 off in the split scratch.
       auto wts = [&](int t, h4_t& bh, h4_t& bl) {
 #pragma unroll
         for (int dw = 0; dw < VD; ++dw) {
@@ -961,7 +998,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
         }
         bh = phi[t / P];
         bl = plo[t / P];
-        if constexpr (P > 1) {
+        if constexpr (P > 1 && !F::QUANT) {
+          const int sh = HG * (t % P);
+          const u2_t h2 = __builtin_bit_cast(u2_t, bh), l2 = __builtin_bit_cast(u2_t, bl);
+          bh = __builtin_bit_cast(h4_t, u2_t{row_shl(h2.x, sh), row_shl(h2.y, sh)});
+          bl = __builtin_bit_cast(h4_t, u2_t{row_shl(l2.x, sh), row_shl(l2.y, sh)});
+        } else if constexpr (P > 1) {
           const bool mine = jl == t % P;
           const u2_t h2 = __builtin_bit_cast(u2_t, bh), l2 = __builtin_bit_cast(u2_t, bl);
           bh = __builtin_bit_cast(h4_t, u2_t{mine ? h2.x : 0u, mine ? h2.y : 0u});
@@ -985,8 +1027,10 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   }
 
   FQKV_STAMP(3);  // last pass's P.V products issued
-  // ---- wave totals: l over the four lane rows; O^T rows are disjoint; the
-  // P columns of a head add up (same running max and shift in all of them) ----
+  // ---- wave totals: l over the four lane rows and the P columns of a head
+  // (same running max and shift in all of them); O^T rows are disjoint; its
+  // columns 0 .. HG - 1 hold every tile (fp16), or the P columns of a head
+  // add up (int8 / int4) ----
   if constexpr (F::QUANT) {
     // acc[c] * vunit = sum w (v + BIAS): take BIAS sum(w) of the column off
     const float wb = F::BIAS * rows4_sum(w_run);
@@ -997,7 +1041,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     l_run = __builtin_amdgcn_ldexpf(l_run, -acc_shift);
   }
   l_run = cols_sum<HG, P>(rows4_sum(l_run));
-  if constexpr (P > 1 && !PVV) {
+  if constexpr (P > 1 && F::QUANT) {
 #pragma unroll
     for (int c = 0; c < VE; ++c)
 #pragma unroll
