@@ -789,10 +789,28 @@ def suite_llama(torch, fq, rows, full=True):
         ts.sort()
         return ts[len(ts) // 2]
 
+    def graphed_s(impl, prompt_len, gen, reps=3):
+        """Best wall time of hf_llama.generate_graphed (prefill, capture and every replay)."""
+        set_impl(impl)
+        ids = torch.randint(0, cfg.vocab_size, (1, prompt_len), device="cuda")
+        hf_llama.generate_graphed(model, ids, 8)
+        torch.cuda.synchronize()
+        best = 1e9
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            hf_llama.generate_graphed(model, ids, gen)
+            torch.cuda.synchronize()
+            best = min(best, time.perf_counter() - t0)
+        return best
+
     r = {"bench": "llama_decode", "config": {"model": "random-init LlamaConfig 16L 2048h 32q/8kv hd64 fp16",
                                              "prompt": 512, "new_tokens": 128}}
     r["sdpa_tok_s"] = round(tok_per_s("sdpa"), 2)
     r["kernel_tok_s"] = round(tok_per_s(name), 2)
+    # every decode step replayed from one HIP graph over a static cache (hf_llama.generate_graphed),
+    # the attention on the paged kernel (kernel) or on transformers' SDPA with its mask (sdpa)
+    r["kernel_graphed_tok_s"] = round(128 / graphed_s(name, 512, 128), 2)
+    r["sdpa_graphed_tok_s"] = round(128 / graphed_s("sdpa", 512, 128), 2)
     if not full:  # generate tok/s only (the reference's end_to_end.json)
         rows.append(r)
         set_impl("sdpa")
@@ -802,6 +820,12 @@ def suite_llama(torch, fq, rows, full=True):
     for ctx in (512, 2048, 8192):
         r["decode_ms_sdpa_ctx%d" % ctx] = round(decode_ms("sdpa", ctx), 4)
         r["decode_ms_kernel_ctx%d" % ctx] = round(decode_ms(name, ctx), 4)
+    # one replayed decode step: the time of 128 more generated tokens over 128 (capacity 1024 at
+    # prompt 512, 16384 at prompt 8192, where the kernel splits over the whole capacity)
+    for ctx in (512, 8192):
+        for impl, key in ((name, "kernel"), ("sdpa", "sdpa")):
+            r["graphed_step_ms_%s_ctx%d" % (key, ctx)] = round(
+                (graphed_s(impl, ctx, 256) - graphed_s(impl, ctx, 128)) / 128 * 1e3, 4)
     # the same hook over an int8 / int4 KV cache (hf_llama.QuantizedKVCache); KV bytes read per
     # decode step at 8192 cached tokens: 16 layers x 2 x 8 heads x 8192 x (128, 64 + 2, 32 + 2) B
     for fmt in ("int8", "int4"):
@@ -815,6 +839,11 @@ def suite_llama(torch, fq, rows, full=True):
                                                  r["decode_ms_kernel_ctx512"], r["decode_ms_sdpa_ctx2048"],
                                                  r["decode_ms_kernel_ctx2048"], r["decode_ms_sdpa_ctx8192"],
                                                  r["decode_ms_kernel_ctx8192"]))
+    log("llama     graphed static cache: generate tok/s sdpa %.2f, kernel %.2f; replayed step ms (sdpa/kernel) "
+        "ctx512 %.3f/%.3f ctx8192 %.3f/%.3f" % (r["sdpa_graphed_tok_s"], r["kernel_graphed_tok_s"],
+                                                r["graphed_step_ms_sdpa_ctx512"], r["graphed_step_ms_kernel_ctx512"],
+                                                r["graphed_step_ms_sdpa_ctx8192"],
+                                                r["graphed_step_ms_kernel_ctx8192"]))
     log("llama     int8 / int4 KV cache: generate tok/s %.2f / %.2f; decode step ms ctx8192 %.3f / %.3f"
         % (r["kernel_int8_tok_s"], r["kernel_int4_tok_s"], r["decode_ms_kernel_int8_ctx8192"],
            r["decode_ms_kernel_int4_ctx8192"]))
@@ -838,7 +867,8 @@ def reference_tables(torch, fq):
     * gqa_aware_n4096_d64 (benchmarks/gqa_aware.json): decode_attn_gqa vs repeat_kv + the
       MHA kernel at Hq 32 / Hkv 8, N 4096, D 64, B in {1, 4, 16};
     * end_to_end_llama (benchmarks/end_to_end.json): generate tok/s at prompt 512 + 128 new
-      tokens on a random-init Llama-3.2-1B-shaped model, SDPA vs the kernel hook (best of 3).
+      tokens on a random-init Llama-3.2-1B-shaped model, SDPA vs the kernel hook (best of 3),
+      and the same with every decode step replayed from a HIP graph over a static cache.
     Each row is gated against fp32 PyTorch on the GPU (max-abs <= 2e-3), loop-timed like the
     suite (400 calls after 40 warm-ups); the reference's A100 numbers ride along."""
     rows = []
@@ -873,6 +903,8 @@ def reference_tables(torch, fq):
         r = rows[0]
         out["end_to_end_llama"] = {"sdpa_tok_s": r["sdpa_tok_s"], "kernel_tok_s": r["kernel_tok_s"],
                                    "speedup": round(r["kernel_tok_s"] / r["sdpa_tok_s"], 3),
+                                   "sdpa_graphed_tok_s": r["sdpa_graphed_tok_s"],
+                                   "kernel_graphed_tok_s": r["kernel_graphed_tok_s"],
                                    "model": r["config"]["model"], "prompt": 512, "new_tokens": 128,
                                    "ref_a100_tok_s": {"sdpa": REF_E2E_TOK_S[0], "kernel": REF_E2E_TOK_S[1]}}
     except ImportError as e:  # transformers absent: the row is skipped, not faked

@@ -184,8 +184,9 @@ __device__ __forceinline__ float wave_sum(float x) {
 // tiles of a pass share one column set: column n holds head n % HG of tile
 // n / HG of each group of P tiles. cols_fold combines the P columns of each
 // head within a 16-lane row (DPP quad_perm xor 1 / xor 2, row_ror 4 / 8);
-// columns past P * HG take part only in HG = 2 and must hold a neutral value
-// (or, for a maximum, any value of the same pass).
+// columns past P * HG take part in HG = 2 and in HG = 1 with P = 8 (whose
+// fold covers the whole row) and must hold a neutral value (or, for a
+// maximum, any value of the same pass).
 // (Sums on fp32 values, maxima on integer keys.)
 template <int HG, int P, typename T, typename Op, typename Mv>
 __device__ __forceinline__ T cols_fold(T x, Op op, Mv mv) {

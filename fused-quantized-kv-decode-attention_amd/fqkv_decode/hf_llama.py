@@ -32,6 +32,17 @@ preallocated cache is a strided view, read in place)::
 
 The prompt's own prefill attends to its exact keys and values; a later call
 with more than one query token attends to the dequantized cache through SDPA.
+
+Graph-captured decoding (no counterpart in the reference, whose decode loop
+pays the host's launch cost for every kernel of every step):
+:func:`StaticKVCache` keeps each layer's keys and values in preallocated
+buffers with the sequence lengths on the device, and the registered
+attention function runs its decode steps on ``decode_attn_gqa_paged`` (each
+sequence's buffer is one page), so no host value changes from one decode
+step to the next and :func:`generate_graphed` captures one whole step of the
+model in a HIP graph and replays it per token::
+
+    tokens = hf_llama.generate_graphed(model, ids, max_new_tokens=128)
 """
 
 import math
@@ -68,6 +79,8 @@ def kernel_applies(query, key, attention_mask, scaling, dropout, **kwargs):
 
 def attention_forward(module, query, key, value, attention_mask=None, scaling=None, dropout=0.0, **kwargs):
     """transformers attention function: query [B, Hq, q, D], key/value [B, Hkv, kv, D] -> ([B, q, Hq, D], None)."""
+    if getattr(key, "fqkv_seq_lens", None) is not None:
+        return _static_attention(module, query, key, value, attention_mask, scaling, dropout, **kwargs)
     if getattr(key, "fqkv_scales", None) is not None:
         return _quantized_attention(module, query, key, value, attention_mask, scaling, dropout, **kwargs)
     if getattr(module, "training", False) or not kernel_applies(query, key, attention_mask, scaling, dropout,
@@ -80,6 +93,25 @@ def attention_forward(module, query, key, value, attention_mask=None, scaling=No
     V = value.to(torch.float16).contiguous()
     out = decode_attn_gqa(q, K, V, _W)                     # [B, Hq, D]
     return out.unsqueeze(1).to(query.dtype), None          # [B, 1, Hq, D]
+
+
+def _static_attention(module, query, key, value, attention_mask, scaling, dropout, **kwargs):
+    """Attention over a StaticKVCache layer's whole buffers [B, Hkv, capacity, D]: a decode step runs the
+    paged kernel over the first seq_lens[b] tokens of sequence b's buffer (one page of ``capacity``
+    tokens; the lengths are read on the device); anything else goes to SDPA with transformers' mask."""
+    B, Hq, qlen, D = query.shape
+    ok = (qlen == 1 and not dropout and not getattr(module, "training", False) and query.is_cuda
+          and key.dtype == torch.float16 and D in (64, 128) and Hq % key.shape[1] == 0
+          and kwargs.get("sliding_window") is None and kwargs.get("softcap") is None
+          and (scaling is None or abs(scaling * math.sqrt(D) - 1.0) <= 1e-6))
+    if not ok:
+        return _sdpa(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
+    from . import decode_attn_gqa_paged
+
+    q = query[:, :, 0, :].to(torch.float16).contiguous()
+    out = decode_attn_gqa_paged(q, key.permute(0, 2, 1, 3), value.permute(0, 2, 1, 3), key.fqkv_page_table,
+                                key.fqkv_seq_lens, key.shape[2], _W)
+    return out.unsqueeze(1).to(query.dtype), None
 
 
 def _quantized_attention(module, query, key, value, attention_mask, scaling, dropout, **kwargs):
@@ -234,6 +266,111 @@ def QuantizedKVCache(config, kv_format="int8", block=256):
 
     text = config.get_text_config(decoder=True) if hasattr(config, "get_text_config") else config
     return Cache(layers=[QuantizedKVLayer(kv_format, block) for _ in range(text.num_hidden_layers)])
+
+
+def _make_static_layer_class():
+    from transformers.cache_utils import StaticLayer
+
+    class DeviceLengthStaticLayer(StaticLayer):
+        """transformers' StaticLayer (keys and values preallocated as [B, Hkv, capacity, D], new
+        tokens written in place at a position kept on the device) that also keeps each sequence's
+        length as a device int32 tensor. The key and value buffers it returns carry the lengths
+        and a one-page-per-sequence page table, which the registered attention function hands
+        to the paged decode kernel: nothing in a decode step reads a length on the host."""
+
+        def __init__(self, max_cache_len):
+            if max_cache_len < 16 or max_cache_len > (1 << 20) or max_cache_len & (max_cache_len - 1):
+                raise ValueError("max_cache_len must be a power of two in [16, 2^20] (one kernel page per "
+                                 "sequence), got %r" % (max_cache_len,))
+            super().__init__(max_cache_len=max_cache_len)
+            self.seq_lens = self.page_table = None
+
+        def lazy_initialization(self, key_states, value_states):
+            super().lazy_initialization(key_states, value_states)
+            B = self.batch_size
+            self.seq_lens = torch.zeros(B, dtype=torch.int32, device=self.device)
+            self.page_table = torch.arange(B, dtype=torch.int32, device=self.device).view(B, 1)
+            for t in (self.keys, self.values):
+                t.fqkv_seq_lens = self.seq_lens
+                t.fqkv_page_table = self.page_table
+
+        def update(self, key_states, value_states, *args, **kwargs):
+            keys, values = super().update(key_states, value_states, *args, **kwargs)
+            self.seq_lens.add_(key_states.shape[-2])
+            return keys, values
+
+        def reset(self):
+            super().reset()
+            if self.is_initialized:
+                self.cumulative_length.zero_()
+                self.seq_lens.zero_()
+
+    return DeviceLengthStaticLayer
+
+
+_STATIC_LAYER_CLASS = None
+
+
+def StaticKVCache(config, max_cache_len):
+    """A transformers ``Cache`` of preallocated fp16 KV buffers with the sequence lengths on the
+    device, for decode steps captured in a HIP graph (:func:`generate_graphed`). ``max_cache_len``
+    (a power of two in [16, 2^20]) bounds prompt plus generated tokens. The batch's sequences must
+    be unpadded: decode steps attend to the first ``length`` positions of each buffer and do not
+    read an attention mask."""
+    from transformers.cache_utils import Cache
+
+    global _STATIC_LAYER_CLASS
+    if _STATIC_LAYER_CLASS is None:
+        _STATIC_LAYER_CLASS = _make_static_layer_class()
+    text = config.get_text_config(decoder=True) if hasattr(config, "get_text_config") else config
+    return Cache(layers=[_STATIC_LAYER_CLASS(max_cache_len) for _ in range(text.num_hidden_layers)])
+
+
+def generate_graphed(model, input_ids, max_new_tokens, max_cache_len=None, use_graph=True):
+    """Greedy decoding with every decode step replayed from one captured HIP graph.
+
+    The prompt runs eagerly into a :func:`StaticKVCache` (capacity ``max_cache_len``, by default the
+    next power of two, at least 16, above prompt + new tokens); the first decode step runs eagerly
+    too (it initialises what the step uses lazily), the second is captured, and every later token
+    is one replay: the graph embeds the token, runs the model on the cache (the attention through
+    the paged kernel when the model's attention implementation is this module's), and writes its
+    argmax back as the next step's input. Unpadded batches only (see :func:`StaticKVCache`).
+    ``use_graph=False`` runs the same steps eagerly. Returns the new tokens, [B, max_new_tokens]."""
+    B, L = input_ids.shape
+    if max_new_tokens < 1:
+        raise ValueError("max_new_tokens must be >= 1")
+    cap = max_cache_len or max(16, 1 << (L + max_new_tokens - 1).bit_length())
+    if L + max_new_tokens > cap:
+        raise ValueError("prompt + new tokens (%d) exceed max_cache_len (%d)" % (L + max_new_tokens, cap))
+    dev = input_ids.device
+    cache = StaticKVCache(model.config, cap)
+    out = torch.empty(B, max_new_tokens, dtype=torch.long, device=dev)
+    with torch.no_grad():
+        logits = model(input_ids, past_key_values=cache, use_cache=True).logits
+        ids = logits[:, -1:].argmax(-1)
+        out[:, :1] = ids
+        pos = torch.full((B, 1), L, dtype=torch.long, device=dev)
+
+        def step():
+            lg = model(ids, past_key_values=cache, position_ids=pos, use_cache=True).logits
+            ids.copy_(lg[:, -1:].argmax(-1))
+            pos.add_(1)
+
+        if max_new_tokens > 1:
+            step()
+            out[:, 1:2] = ids
+        if max_new_tokens > 2 and not use_graph:
+            for i in range(2, max_new_tokens):
+                step()
+                out[:, i:i + 1] = ids
+        elif max_new_tokens > 2:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                step()
+            for i in range(2, max_new_tokens):
+                graph.replay()
+                out[:, i:i + 1] = ids
+    return out
 
 
 def register(name=DEFAULT_NAME):

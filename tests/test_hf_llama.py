@@ -252,3 +252,67 @@ def test_gpu_generate_with_quantized_cache_runs_the_kernel(monkeypatch):
                              past_key_values=hf_llama.QuantizedKVCache(model.config, "int8", block=64))
     assert out.shape == (1, 320)
     assert calls["n"] == 2 * 299  # every decode step of both layers (the capacity grows past 256 on the way)
+
+
+def test_static_cache_rejects_a_capacity_the_kernel_cannot_page():
+    cfg = transformers.LlamaConfig(vocab_size=100, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, head_dim=32)
+    for bad in (0, 8, 100, 3 << 10, 1 << 21):
+        with pytest.raises(ValueError, match="power of two"):
+            hf_llama.StaticKVCache(cfg, bad)
+    assert len(hf_llama.StaticKVCache(cfg, 64).layers) == 2
+
+
+def test_static_cache_cpu_decode_matches_dynamic_cache():
+    """On CPU every call goes to SDPA; the static cache (lengths on the device, positions passed
+    in) must reproduce generate()'s greedy tokens over the dynamic cache."""
+    model = tiny_llama(layers=2, hidden=256, heads=4, kv_heads=2)
+    ids = torch.randint(0, 1000, (2, 12), generator=torch.Generator().manual_seed(3))
+    set_impl(model, hf_llama.register())
+    with torch.no_grad():
+        base = model.generate(ids, max_new_tokens=6, do_sample=False)[:, 12:]
+        cache = hf_llama.StaticKVCache(model.config, 32)
+        tok = model(ids, past_key_values=cache, use_cache=True).logits[:, -1:].argmax(-1)
+        toks, pos = [tok], torch.full((2, 1), 12, dtype=torch.long)
+        for _ in range(5):
+            tok = model(tok, past_key_values=cache, position_ids=pos, use_cache=True).logits[:, -1:].argmax(-1)
+            toks.append(tok)
+            pos += 1
+    assert torch.equal(base, torch.cat(toks, 1))
+    assert cache.layers[0].seq_lens.tolist() == [17, 17]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("geometry", sorted(GEOMETRIES))
+def test_gpu_graphed_generation(geometry, monkeypatch):
+    """generate_graphed: every decode step after the second is a replay of one captured HIP graph
+    whose attention is the paged kernel reading the lengths on the device. The replayed tokens
+    equal the same steps run eagerly, bit for bit, and SDPA's greedy tokens (a divergence only at
+    an SDPA tie); the captured step called the paged kernel in every layer."""
+    name = hf_llama.register()
+    model = tiny_llama(dtype=torch.float16, device="cuda", **GEOMETRIES[geometry])
+    ids = torch.randint(0, model.config.vocab_size, (1, 45), generator=torch.Generator().manual_seed(4)).cuda()
+    set_impl(model, "sdpa")
+    base, margins = greedy(model, ids, 40)
+    set_impl(model, name)
+    import fqkv_decode
+    calls = {"n": 0}
+    real = fqkv_decode.decode_attn_gqa_paged
+
+    def counted(*a, **k):
+        calls["n"] += 1
+        return real(*a, **k)
+
+    monkeypatch.setattr(fqkv_decode, "decode_attn_gqa_paged", counted)
+    eager = hf_llama.generate_graphed(model, ids, 40, use_graph=False)
+    n_eager = calls["n"]
+    graphed = hf_llama.generate_graphed(model, ids, 40)
+    layers = model.config.num_hidden_layers
+    assert n_eager == 39 * layers          # every decode step, every layer
+    assert calls["n"] - n_eager == 2 * layers  # the eager first step and the captured one
+    assert torch.equal(graphed, eager)
+    ours = graphed[0].tolist()
+    for i, (a, b) in enumerate(zip(base, ours)):
+        if a != b:
+            assert margins[i] < 1e-2, ("divergence at step %d without a tie" % i, margins[i])
+            break
