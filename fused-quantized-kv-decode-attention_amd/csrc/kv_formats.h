@@ -112,22 +112,23 @@ __device__ __forceinline__ auto buf_load(rsrc_t r, uint32_t off, uint32_t soff =
 
 // V chunk of VBYTES bytes as VD dwords (a 2-byte chunk is zero-extended).
 // V rows are read whole by one instruction stream and never again: the loads
-// carry the non-temporal hint.
-template <int VBYTES, int VD>
+// carry the non-temporal hint (CP = CPOL_NT) unless the caller asks for none
+// (CP = 0).
+template <int VBYTES, int VD, int CP = CPOL_NT>
 __device__ __forceinline__ void load_vchunk(rsrc_t r, uint32_t off, uint32_t (&d)[VD], uint32_t soff = 0) {
   if constexpr (VBYTES == 16) {
     const u4_t v =
-        __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, CPOL_NT));
+        __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, CP));
 #pragma unroll
     for (int k = 0; k < 4; ++k) d[k] = v[k];
   } else if constexpr (VBYTES == 8) {
-    const u2_t v = __builtin_bit_cast(u2_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, (int)soff, CPOL_NT));
+    const u2_t v = __builtin_bit_cast(u2_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, (int)soff, CP));
     d[0] = v[0];
     d[1] = v[1];
   } else if constexpr (VBYTES == 4) {
-    d[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, (int)soff, CPOL_NT);
+    d[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, (int)soff, CP);
   } else {
-    d[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, (int)soff, CPOL_NT);
+    d[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, (int)soff, CP);
   }
 }
 
