@@ -662,6 +662,19 @@ def suite_paged(torch, fq, steps, warmup, rows):
         cfg = {"B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": Dd, "W": W, "fmt": fmt}
         rows.append(_row("gqa_contiguous_" + fmt, cfg, ms, nbytes, err))
         log("paged suite: contiguous %s        %8.2f us  %7.1f GB/s  err %.2e" % (fmt, ms * 1e3, nbytes / ms / 1e6, err))
+        # the same tokens token-major without pages (FlashInfer's NHD, [B, N, Hkv, ...])
+        tm = lambda X: X.view(B, Hkv, N, *X.shape[2:]).transpose(1, 2).contiguous()
+        Kt, Vt = tm(K), tm(V)
+        Kst, Vst = (tm(Ks), tm(Vs)) if Ks is not None else (None, None)
+        fn = lambda i: fq.decode_attn_gqa_nhd(q, Kt, Vt, W, Kst, Vst)
+        on = fn(0)
+        nerr = float((on[0].float() - ref0).abs().max())
+        same = bool(torch.equal(on, o))
+        ms = _loop_ms(torch, fn, 1, nsteps, nwarm)
+        rows.append(_row("gqa_nhd_" + fmt, cfg, ms, nbytes, nerr, equal_to_contiguous=same))
+        log("paged suite: token-major %s       %8.2f us  %7.1f GB/s  err %.2e  equal to contiguous: %s"
+            % (fmt, ms * 1e3, nbytes / ms / 1e6, nerr, same))
+        del Kt, Vt, Kst, Vst
         for page, hnd in ((16, False), (64, False), (256, False), (64, True)):
             npb = N // page
             P = B * npb

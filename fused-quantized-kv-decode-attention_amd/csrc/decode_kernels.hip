@@ -559,7 +559,9 @@ constexpr int tiles_per_pass() {
   return (FMT == KV_I4 && D == 64 && HG == 1 && !PAGED && !PVV) ? 8 : 4;
 }
 
-template <int FMT, int D, int HG, bool PAGED, bool PVV = false>
+// KEEPV: int4 rows token-major without pages (heads sharing cache lines, the
+// launcher's head grouping on), whose V loads go without the non-temporal hint.
+template <int FMT, int D, int HG, bool PAGED, bool PVV = false, bool KEEPV = false>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
   static_assert(!PVV || (FMT == KV_F16 && !PAGED), "P.V on the vector ALUs: fp16, contiguous rows");
@@ -808,11 +810,11 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
         for (int k = 0; k < 4; ++k) ks[g][k] = vs[g][k] = (_Float16)1.0f;
     }
-    // paged int4 V without the non-temporal hint: in token-major pages the 64-byte rows of two
-    // KV heads share each cache line, read in turn by workgroups on one XCD (batch 8, N 32768:
-    // 68.6 -> 55.1 us; head-major pages flat). Everywhere else the hint is faster (without it
-    // int8 / int4 MHA at B 2048 +10 %, paged int8 +18 %).
-    constexpr int VCP = (PAGED && FMT == KV_I4) ? 0 : CPOL_NT;
+    // paged and token-major int4 V without the non-temporal hint: there the 64-byte rows of
+    // two KV heads share each cache line, read in turn by workgroups on one XCD (paged, batch 8,
+    // N 32768: 68.6 -> 55.1 us; head-major pages flat). Everywhere else the hint is faster
+    // (without it int8 / int4 MHA at B 2048 +10 %, paged int8 +18 %).
+    constexpr int VCP = (FMT == KV_I4 && (PAGED || KEEPV)) ? 0 : CPOL_NT;
 #pragma unroll
     for (int u = 0; u < U; ++u) {
 #pragma unroll
@@ -1212,6 +1214,9 @@ static hipError_t launch_partial_t(const PartialParams& p, int nblocks, int nw, 
   }
   if (p.page_table)
     hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, true>), dim3(nblocks), dim3(64 * nw), lds, st, p);
+  else if (FMT == KV_I4 && p.hg_k)
+    hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false, false, FMT == KV_I4>), dim3(nblocks), dim3(64 * nw),
+                       lds, st, p);
   else
     hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false>), dim3(nblocks), dim3(64 * nw), lds, st, p);
   return hipGetLastError();
