@@ -56,7 +56,9 @@ constexpr int MAX_DEV = 64;
 // per-thread default stream (one handle for many streams), get the
 // two-kernel merge, which uses no library state.
 std::atomic<int> g_force_two_kernel{0};
-constexpr int EAGER_SLOTS = 12;  // slots 0 .. 11 for eager calls, 12 .. 15 for captures
+// slots 0 .. 11 for eager calls, 12 .. 127 for captures (an engine that captures a graph
+// per batch size keeps the one-kernel merge in every graph); 64 KiB of counters each
+constexpr int EAGER_SLOTS = 12;
 
 struct SlotTable {
   std::mutex mu;

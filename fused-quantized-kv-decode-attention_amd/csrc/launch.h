@@ -101,7 +101,7 @@ inline void set_contiguous_layout(PartialParams& p, int64_t rows, int64_t N, int
 
 // In-kernel split merge: each call with S > 1 takes one of SPLIT_SLOTS slots
 // of MAX_SPLIT_GROUPS arrival counters (one per (KV row, head group)).
-constexpr int SPLIT_SLOTS = 16;
+constexpr int SPLIT_SLOTS = 128;
 constexpr int MAX_SPLIT_GROUPS = 16384;
 
 hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& p, int nblocks, int nw,

@@ -290,9 +290,9 @@ int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, v
  * and the internal splits of the single-block entry points). Default (0):
  * one kernel per call; the last workgroup of each head group to finish merges
  * that group's split partials, using library-owned arrival counters. The
- * counters come in 16 slots per device: each stream keeps one of 12 slots for
+ * counters come in 128 slots per device: each stream keeps one of 12 slots for
  * its eager calls (first come, first served), and each stream capture takes
- * one of the other 4 for the graph it records; calls on a stream or capture
+ * one of the other 116 for the graph it records; calls on a stream or capture
  * with no free slot, and calls on hipStreamPerThread, use the two-kernel
  * merge. So calls that may overlap never share a slot; the one exception a
  * caller must avoid is replaying one captured graph on two streams at once

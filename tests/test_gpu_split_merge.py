@@ -77,6 +77,36 @@ def test_graph_replays_beside_eager_calls_on_a_side_stream():
         assert torch.equal(a[4], ref_a)
 
 
+def test_many_captured_graphs_replay_in_turn():
+    """Ten captured split-K graphs, more captures than the four slots the
+    registry once reserved for them, replayed in turn for three rounds with an
+    eager split call and a synchronisation between replays: every replay
+    equals its call run eagerly."""
+    g = torch.Generator().manual_seed(63)
+    calls = [make_call(g, N=1200 + 100 * i, S=8 + i) for i in range(10)]
+    alone = []
+    for c in calls:
+        run(c)
+        alone.append(c[4].clone())
+    graphs = []
+    for c in calls:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run(c)
+        graphs.append(graph)
+    extra = make_call(g, N=900, S=12)
+    run(extra)
+    ref_extra = extra[4].clone()
+    for _ in range(3):
+        for c, graph, ref in zip(calls, graphs, alone):
+            c[4].zero_()
+            graph.replay()
+            run(extra)
+            torch.cuda.synchronize()
+            assert torch.equal(c[4], ref)
+            assert torch.equal(extra[4], ref_extra)
+
+
 def test_more_streams_than_merge_slots():
     """Split calls in flight on 20 streams at once, more than there are eager
     slots: streams beyond them merge with the two-kernel form, and every
