@@ -261,11 +261,19 @@ int check_ptrs_quant(int fmt, int64_t D, const void* q, const void* K, const voi
 // The kernels address a KV row block with 32-bit byte offsets.
 int64_t row_bytes_of(int fmt, int64_t D);
 
+// Byte offsets inside a KV row are 32-bit, formed in the kernel as tile offset
+// + lane offset (for int4 summed by the load itself, the tile offset in the
+// SGPR offset). A pass of a wave addresses up to 8 tiles spaced 16 tokens x 8
+// waves apart even where they lie past the end of the row (those loads return
+// zeros), so the row plus 8 x 128 + 16 tokens must fit in 4 GiB: then no offset,
+// in the kernel or in the load's own sum, reaches 2^32.
+constexpr int64_t ROW_SPAN = int64_t(1) << 32;
+constexpr int64_t SPAN_MARGIN_TOKENS = 8 * 16 * 8 + 16;
 int check_span(int64_t N, int64_t D, int fmt) {
   const int64_t row_bytes = row_bytes_of(fmt, D);
-  if (N * row_bytes > (int64_t)UINT32_MAX)
-    return fail(FQKV_ERR_ARG, "N: %lld tokens of %lld bytes exceed the 4 GiB per-row span", (long long)N,
-                (long long)row_bytes);
+  if ((N + SPAN_MARGIN_TOKENS) * row_bytes > ROW_SPAN)
+    return fail(FQKV_ERR_ARG, "N: %lld tokens of %lld bytes exceed the per-row span (4 GiB less %lld tokens)",
+                (long long)N, (long long)row_bytes, (long long)SPAN_MARGIN_TOKENS);
   return FQKV_OK;
 }
 
@@ -554,9 +562,10 @@ int fqkv_decode_attn_gqa_strided(const void* q, const void* K, const void* V, co
   if ((rc = check_layout_common(kv_format, D, q, K, V, Ks, Vs, o, kv_batch_stride, kv_head_stride,
                                 kv_token_stride, sc_batch_stride, sc_head_stride, sc_token_stride)))
     return rc;
-  if (N * kv_token_stride > (int64_t)UINT32_MAX || (kv_format != KV_F16 && 2 * N * sc_token_stride > (int64_t)UINT32_MAX))
-    return fail(FQKV_ERR_ARG, "N: %lld tokens at a %lld-byte stride exceed the 4 GiB per-row span", (long long)N,
-                (long long)kv_token_stride);
+  if ((N + SPAN_MARGIN_TOKENS) * kv_token_stride > ROW_SPAN ||
+      (kv_format != KV_F16 && 2 * (N + SPAN_MARGIN_TOKENS) * sc_token_stride > ROW_SPAN))
+    return fail(FQKV_ERR_ARG, "N: %lld tokens at a %lld-byte stride exceed the per-row span (4 GiB less %lld tokens)",
+                (long long)N, (long long)kv_token_stride, (long long)SPAN_MARGIN_TOKENS);
   Layout L{Hkv, kv_batch_stride, kv_head_stride, kv_token_stride, sc_batch_stride, sc_head_stride, sc_token_stride,
            nullptr, nullptr, 0, 0, 0};
   return run_decode(kv_format, q, K, V, Ks, Vs, o, B * Hkv, Hq / Hkv, N, D, W, workspace, workspace_bytes,

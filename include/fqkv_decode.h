@@ -21,7 +21,8 @@
  *   softmax scale  = 1.0f / sqrtf((float)D); D (head_dim) is 64 or 128
  *
  * Alignment: q, K, V and o_part 16 bytes (K, V 8 bytes for int4 at D = 64);
- * o, scales 2 bytes. Each K or V row block (N rows) must span < 4 GiB.
+ * o, scales 2 bytes. Each K or V row block, N rows plus 1040 more, must span
+ * at most 4 GiB (fp16 at D = 128: N <= 2^24 - 1040 tokens per KV head).
  *
  * W (and CW) count 64-lane waves per workgroup. W is a maximum: a split too
  * short to give every wave a full pass of 4 16-token tiles runs on fewer
@@ -182,8 +183,8 @@ int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const vo
  * reference layout; [B, N, Hkv, D] (FlashInfer's NHD, flashinfer_looptimed.py:63-65)
  * has kv_token_stride = Hkv*row_bytes, kv_head_stride = row_bytes,
  * kv_batch_stride = N*Hkv*row_bytes. q [B, Hq, D], o [B, Hq, D] fp16.
- * Strides are multiples of 16 bytes (8 for int4 at D = 64); N * kv_token_stride
- * < 4 GiB. No counterpart in the reference (contiguous [B, Hkv, N, D] only).
+ * Strides are multiples of 16 bytes (8 for int4 at D = 64); (N + 1040) *
+ * kv_token_stride <= 4 GiB. No counterpart in the reference (contiguous [B, Hkv, N, D] only).
  */
 int fqkv_decode_attn_gqa_strided(const void* q, const void* K, const void* V, const void* Ks, const void* Vs,
                                  void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t N, int64_t D, int kv_format,

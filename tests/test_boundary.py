@@ -228,3 +228,28 @@ def test_capi_noalloc_rejects_before_any_hip_call(lib):
     assert _err(lib).startswith("S:")
     assert f(p, p, p, p, 30, 8, 1024, 128, 4, 8, 8, None) == 1
     assert _err(lib).startswith("heads:")
+
+
+def test_capi_rejects_rows_past_the_32_bit_span(lib):
+    """Byte offsets inside a KV row are 32-bit, and a pass addresses tiles up to 8 x 128 + 16
+    tokens past the end of the row: the row plus that margin must fit in 4 GiB. One token
+    more than the longest accepted row (2^32 / row bytes - 1040 tokens) is rejected before
+    any HIP call."""
+    fs = lib.fqkv_gqa_sk_fast
+    fs.argtypes = [VP] * 7 + [I64] * 7 + [VP]
+    assert fs(*[16] * 7, 4, 1, (1 << 24) - 1039, 128, 16, 8, 8, None) == 1  # fp16 rows of 256 B
+    assert _err(lib).startswith("N:") and "4 GiB" in _err(lib), _err(lib)
+    f4 = lib.fqkv_decode_attn_int4
+    f4.argtypes = [VP, VP, VP, VP, VP, VP, I64, I64, I64, I64, VP, ctypes.c_size_t, VP]
+    assert f4(*[16] * 6, 1, (1 << 26) - 1039, 128, 8, None, 0, None) == 1  # int4 rows of 64 B
+    assert _err(lib).startswith("N:") and "4 GiB" in _err(lib), _err(lib)
+    f8 = lib.fqkv_decode_attn_int8_mw
+    f8.argtypes = f4.argtypes
+    assert f8(*[16] * 6, 1, (1 << 25) - 1039, 128, 8, None, 0, None) == 1  # int8 rows of 128 B
+    assert _err(lib).startswith("N:") and "4 GiB" in _err(lib), _err(lib)
+    fst = lib.fqkv_decode_attn_gqa_strided
+    fst.argtypes = [VP] * 6 + [I64] * 5 + [ctypes.c_int] + [I64] * 7 + [VP, ctypes.c_size_t, VP]
+    # token-major fp16, Hkv 8 x 256-byte rows: a 2 KiB token stride
+    assert fst(16, 16, 16, None, None, 16, 1, 32, 8, (1 << 21) - 1039, 128, 0, 8 << 21, 256, 2048,
+               0, 0, 1, 8, None, 0, None) == 1
+    assert _err(lib).startswith("N:") and "4 GiB" in _err(lib), _err(lib)
