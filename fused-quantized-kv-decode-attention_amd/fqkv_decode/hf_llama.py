@@ -100,7 +100,10 @@ def _static_attention(module, query, key, value, attention_mask, scaling, dropou
     paged kernel over the first seq_lens[b] tokens of sequence b's buffer (one page of ``capacity``
     tokens; the lengths are read on the device); anything else goes to SDPA with transformers' mask."""
     B, Hq, qlen, D = query.shape
+    # a caller's padding mask (folded into transformers' mask by the builder register() installs)
+    # may hide positions below the length: that step goes to SDPA with the mask
     ok = (qlen == 1 and not dropout and not getattr(module, "training", False) and query.is_cuda
+          and not getattr(attention_mask, "fqkv_padding", False)
           and key.dtype == torch.float16 and D in (64, 128) and Hq % key.shape[1] == 0
           and kwargs.get("sliding_window") is None and kwargs.get("softcap") is None
           and (scaling is None or abs(scaling * math.sqrt(D) - 1.0) <= 1e-6))
@@ -314,9 +317,10 @@ _STATIC_LAYER_CLASS = None
 def StaticKVCache(config, max_cache_len):
     """A transformers ``Cache`` of preallocated fp16 KV buffers with the sequence lengths on the
     device, for decode steps captured in a HIP graph (:func:`generate_graphed`). ``max_cache_len``
-    (a power of two in [16, 2^20]) bounds prompt plus generated tokens. The batch's sequences must
-    be unpadded: decode steps attend to the first ``length`` positions of each buffer and do not
-    read an attention mask."""
+    (a power of two in [16, 2^20]) bounds prompt plus generated tokens. Decode steps on the kernel
+    attend to the first ``length`` positions of each buffer and read no attention mask, so a call
+    that passes a padding mask runs its decode steps on SDPA instead (still correct, not
+    graph-replayed by :func:`generate_graphed`, which passes none)."""
     from transformers.cache_utils import Cache
 
     global _STATIC_LAYER_CLASS
@@ -334,7 +338,8 @@ def generate_graphed(model, input_ids, max_new_tokens, max_cache_len=None, use_g
     too (it initialises what the step uses lazily), the second is captured, and every later token
     is one replay: the graph embeds the token, runs the model on the cache (the attention through
     the paged kernel when the model's attention implementation is this module's), and writes its
-    argmax back as the next step's input. Unpadded batches only (see :func:`StaticKVCache`).
+    argmax back as the next step's input. The prompt rows are taken as unpadded (no attention mask
+    is passed).
     ``use_graph=False`` runs the same steps eagerly. Returns the new tokens, [B, max_new_tokens]."""
     B, L = input_ids.shape
     if max_new_tokens < 1:
@@ -373,11 +378,21 @@ def generate_graphed(model, input_ids, max_new_tokens, max_cache_len=None, use_g
     return out
 
 
+def _sdpa_mask(*args, **kwargs):
+    """transformers' SDPA mask builder; a mask that folds in a caller's 2-D padding mask is tagged
+    ``fqkv_padding`` so the static-cache decode path, which reads no mask, leaves it to SDPA."""
+    from transformers.masking_utils import sdpa_mask
+
+    mask = sdpa_mask(*args, **kwargs)
+    if mask is not None and kwargs.get("attention_mask") is not None:
+        mask.fqkv_padding = True
+    return mask
+
+
 def register(name=DEFAULT_NAME):
     """Register the attention function (and the SDPA mask builder) under ``name``; returns ``name``."""
     from transformers import AttentionInterface, AttentionMaskInterface
-    from transformers.masking_utils import sdpa_mask
 
     AttentionInterface.register(name, attention_forward)
-    AttentionMaskInterface.register(name, sdpa_mask)
+    AttentionMaskInterface.register(name, _sdpa_mask)
     return name

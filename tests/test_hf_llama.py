@@ -316,3 +316,38 @@ def test_gpu_graphed_generation(geometry, monkeypatch):
         if a != b:
             assert margins[i] < 1e-2, ("divergence at step %d without a tie" % i, margins[i])
             break
+
+
+@pytest.mark.gpu
+def test_gpu_static_cache_with_a_padding_mask_goes_to_sdpa(monkeypatch):
+    """A left-padded batch over the static cache: the decode step's mask folds in the padding,
+    so the registered function hands the step to SDPA with that mask instead of the kernel, which
+    reads no mask (the paged kernel is not called); its logits equal SDPA's over the same cache."""
+    name = hf_llama.register()
+    import fqkv_decode
+    calls = {"n": 0}
+    real = fqkv_decode.decode_attn_gqa_paged
+
+    def counted(*a, **k):
+        calls["n"] += 1
+        return real(*a, **k)
+
+    monkeypatch.setattr(fqkv_decode, "decode_attn_gqa_paged", counted)
+    model = tiny_llama(layers=2, dtype=torch.float16, device="cuda")
+    ids = torch.randint(0, 1000, (2, 20), generator=torch.Generator().manual_seed(5)).cuda()
+    mask = torch.ones(2, 20, dtype=torch.long, device="cuda")
+    mask[1, :7] = 0  # row 1 left-padded by 7 tokens
+    step = torch.randint(0, 1000, (2, 1), generator=torch.Generator().manual_seed(6)).cuda()
+    step_mask = torch.cat([mask, torch.ones(2, 1, dtype=torch.long, device="cuda")], 1)
+    pos = mask.sum(1, keepdim=True)  # the new token's position in each row
+    prefill_pos = (mask.cumsum(1) - 1).clamp(min=0)
+    outs = {}
+    for impl in ("sdpa", name):
+        set_impl(model, impl)
+        cache = hf_llama.StaticKVCache(model.config, 32)
+        with torch.no_grad():
+            model(ids, attention_mask=mask, position_ids=prefill_pos, past_key_values=cache, use_cache=True)
+            outs[impl] = model(step, attention_mask=step_mask, position_ids=pos, past_key_values=cache,
+                               use_cache=True).logits.float()
+    assert calls["n"] == 0
+    assert float((outs[name] - outs["sdpa"]).abs().max()) <= 1e-3
