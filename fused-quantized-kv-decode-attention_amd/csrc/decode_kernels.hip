@@ -10,9 +10,10 @@
 // split's last token, so rows past it read as zeros and need no clamping),
 // then consumes the tiles in order while the later ones are still arriving.
 // Per tile a wave
-//   1. has loaded the K tile as matrix-core operand A (lane l: token l % 16,
-//      64 contiguous bytes of 16 rows per dwordx4 instruction) and the V tile
-//      as four loads of 4 whole rows each,
+//   1. has loaded the K tile as matrix-core operand A (int8 / int4: lane l
+//      token l % 16, 64 contiguous bytes of 16 rows per dwordx4 instruction;
+//      fp16: whole rows, rearranged through the wave's LDS rows) and the V
+//      tile as four loads of 4 whole rows each,
 //   2. computes the transposed scores S^T = K Q^T (tokens on M, query heads
 //      on N) with D/32 v_mfma_f32_16x16x32_f16; column n carries head
 //      n % HG, and lane l keeps the scores of tile (l % 16) / HG of each
@@ -26,7 +27,10 @@
 //      after a 4 x 4 exchange of the V chunks between lane rows and
 //      registers (v_permlane32_swap / v_permlane16_swap) puts four tokens of
 //      one head-dim element in each operand slot; int8/int4 become exact
-//      fp16 on the way.
+//      fp16 on the way. Each tile's weights enter operand B in the columns
+//      0 .. HG-1 that are emitted (fp16: moved there by a DPP row shift) or
+//      in the tile's own columns, the rest zero, summed at the end (int8 /
+//      int4, whose products carry a bias until then).
 // Waves of a workgroup take interleaved tiles; their (m, l, acc) states are
 // merged through LDS. With one split the workgroup writes the normalised
 // fp16 output; otherwise it writes the reference's fp32 scratch layout
