@@ -802,16 +802,16 @@ def suite_llama(torch, fq, rows, full=True):
         ts.sort()
         return ts[len(ts) // 2]
 
-    def graphed_s(impl, prompt_len, gen, reps=3):
+    def graphed_s(impl, prompt_len, gen, reps=3, kv_format=None):
         """Best wall time of hf_llama.generate_graphed (prefill, capture and every replay)."""
         set_impl(impl)
         ids = torch.randint(0, cfg.vocab_size, (1, prompt_len), device="cuda")
-        hf_llama.generate_graphed(model, ids, 8)
+        hf_llama.generate_graphed(model, ids, 8, kv_format=kv_format)
         torch.cuda.synchronize()
         best = 1e9
         for _ in range(reps):
             t0 = time.perf_counter()
-            hf_llama.generate_graphed(model, ids, gen)
+            hf_llama.generate_graphed(model, ids, gen, kv_format=kv_format)
             torch.cuda.synchronize()
             best = min(best, time.perf_counter() - t0)
         return best
@@ -844,6 +844,10 @@ def suite_llama(torch, fq, rows, full=True):
     for fmt in ("int8", "int4"):
         r["kernel_%s_tok_s" % fmt] = round(tok_per_s(name, kv_format=fmt), 2)
         r["decode_ms_kernel_%s_ctx8192" % fmt] = round(decode_ms(name, 8192, kv_format=fmt), 4)
+        # graph-replayed over a static int8 / int4 cache (device-position append + paged kernel)
+        r["kernel_graphed_%s_tok_s" % fmt] = round(128 / graphed_s(name, 512, 128, kv_format=fmt), 2)
+        r["graphed_step_ms_kernel_%s_ctx8192" % fmt] = round(
+            (graphed_s(name, 8192, 256, kv_format=fmt) - graphed_s(name, 8192, 128, kv_format=fmt)) / 128 * 1e3, 4)
     r["kv_mb_per_step_ctx8192"] = {f: round(16 * 2 * 8 * 8192 * b / 1e6, 1)
                                    for f, b in (("fp16", 128), ("int8", 66), ("int4", 34))}
     rows.append(r)
@@ -857,9 +861,11 @@ def suite_llama(torch, fq, rows, full=True):
                                                 r["graphed_step_ms_sdpa_ctx512"], r["graphed_step_ms_kernel_ctx512"],
                                                 r["graphed_step_ms_sdpa_ctx8192"],
                                                 r["graphed_step_ms_kernel_ctx8192"]))
-    log("llama     int8 / int4 KV cache: generate tok/s %.2f / %.2f; decode step ms ctx8192 %.3f / %.3f"
+    log("llama     int8 / int4 KV cache: generate tok/s %.2f / %.2f; decode step ms ctx8192 %.3f / %.3f; "
+        "graphed tok/s %.2f / %.2f, replayed step ms ctx8192 %.3f / %.3f"
         % (r["kernel_int8_tok_s"], r["kernel_int4_tok_s"], r["decode_ms_kernel_int8_ctx8192"],
-           r["decode_ms_kernel_int4_ctx8192"]))
+           r["decode_ms_kernel_int4_ctx8192"], r["kernel_graphed_int8_tok_s"], r["kernel_graphed_int4_tok_s"],
+           r["graphed_step_ms_kernel_int8_ctx8192"], r["graphed_step_ms_kernel_int4_ctx8192"]))
     set_impl("sdpa")
     del model
     torch.cuda.empty_cache()

@@ -682,7 +682,39 @@ int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, v
   if (!aligned(K_cache, qal) || !aligned(V_cache, qal)) return fail(FQKV_ERR_ARG, "caches must be %d-byte aligned", (int)qal);
   if (!aligned(Ks_cache, 2) || !aligned(Vs_cache, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
   hipError_t e = launch_quantize_append(x_dtype == FQKV_SRC_F16, kv_format, (int)D, K_new, V_new, K_cache, V_cache,
-                                        Ks_cache, Vs_cache, rows, n_new, capacity, pos, (hipStream_t)stream);
+                                        Ks_cache, Vs_cache, rows, n_new, capacity, pos, nullptr, 1,
+                                        (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "launch: quantize append kernel");
+  return FQKV_OK;
+}
+
+int fqkv_quantize_kv_append_at(const void* K_new, const void* V_new, int x_dtype, void* K_cache, void* V_cache,
+                               void* Ks_cache, void* Vs_cache, int64_t rows, int64_t n_new, int64_t capacity,
+                               const int32_t* pos, int64_t rows_per_pos, int64_t D, int kv_format, void* stream) {
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32)
+    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16 or FQKV_SRC_F32");
+  if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
+  if (rows < 1 || n_new < 1) return fail(FQKV_ERR_ARG, "rows and n_new must be >= 1, got %lld and %lld",
+                                         (long long)rows, (long long)n_new);
+  if (capacity < 1 || n_new > capacity)
+    return fail(FQKV_ERR_ARG, "pos: %lld new tokens do not fit a capacity of %lld", (long long)n_new,
+                (long long)capacity);
+  if (rows_per_pos < 1 || rows % rows_per_pos != 0)
+    return fail(FQKV_ERR_ARG, "pos: rows_per_pos (%lld) must divide rows (%lld)", (long long)rows_per_pos,
+                (long long)rows);
+  if (!K_new || !V_new || !K_cache || !V_cache || !Ks_cache || !Vs_cache || !pos)
+    return fail(FQKV_ERR_ARG, "null tensor pointer");
+  const uintptr_t xal = (x_dtype == FQKV_SRC_F16 && D == 64) ? 8 : 16;
+  const uintptr_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
+  if (!aligned(K_new, xal) || !aligned(V_new, xal)) return fail(FQKV_ERR_ARG, "K_new and V_new must be %d-byte aligned", (int)xal);
+  if (!aligned(K_cache, qal) || !aligned(V_cache, qal)) return fail(FQKV_ERR_ARG, "caches must be %d-byte aligned", (int)qal);
+  if (!aligned(Ks_cache, 2) || !aligned(Vs_cache, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
+  if (!aligned(pos, 4)) return fail(FQKV_ERR_ARG, "pos must be 4-byte aligned");
+  hipError_t e = launch_quantize_append(x_dtype == FQKV_SRC_F16, kv_format, (int)D, K_new, V_new, K_cache, V_cache,
+                                        Ks_cache, Vs_cache, rows, n_new, capacity, 0, pos, rows_per_pos,
+                                        (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "launch: quantize append kernel");
   return FQKV_OK;
 }

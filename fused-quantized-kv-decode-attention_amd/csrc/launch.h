@@ -118,6 +118,6 @@ hipError_t launch_quantize(int src_f16, int fmt, int D, const void* X, void* Q, 
                            hipStream_t st);
 hipError_t launch_quantize_append(int src_f16, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,
                                   void* Sk, void* Sv, int64_t rows, int64_t n, int64_t cap, int64_t pos,
-                                  hipStream_t st);
+                                  const int32_t* pos_of, int64_t rows_per_pos, hipStream_t st);
 
 }  // namespace fqkv

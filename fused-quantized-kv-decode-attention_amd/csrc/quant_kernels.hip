@@ -179,21 +179,32 @@ __global__ void __launch_bounds__(256) quantize_kernel(const void* __restrict__ 
 // Append form for a live cache: K and V rows of `rows` cache rows x n new
 // tokens ([rows, n, D] each, contiguous) go to token positions pos .. pos+n-1
 // of caches laid out [rows, cap, D or D/2] with scales [rows, cap]. One launch
-// covers both tensors: row index j < rows*n is K, the rest V.
+// covers both tensors: row index j < rows*n is K, the rest V. With pos_of set,
+// the position of cache row r is pos_of[r / rows_per_pos] instead, read on the
+// device (so a captured graph appends where the cache currently ends); rows
+// whose tokens would not fit in [0, cap) are not written.
 template <bool F16, int QMAX, int D>
 __global__ void __launch_bounds__(256) quantize_append_kernel(const void* __restrict__ Xk, const void* __restrict__ Xv,
                                                               uint8_t* __restrict__ Qk, uint8_t* __restrict__ Qv,
                                                               _Float16* __restrict__ Sk, _Float16* __restrict__ Sv,
-                                                              int64_t tokens, int64_t n, int64_t cap, int64_t pos) {
+                                                              int64_t tokens, int64_t n, int64_t cap, int64_t pos,
+                                                              const int32_t* __restrict__ pos_of, int64_t rows_per_pos) {
   const int i = threadIdx.x & 15;
   const int64_t rows_per_step = (int64_t)gridDim.x * (blockDim.x >> 4);
   for (int64_t j = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
        j - (threadIdx.x >> 4) < 2 * tokens; j += rows_per_step) {
+    const bool in = j < 2 * tokens;  // the same for the 16 lanes of a row
     const bool v = j >= tokens;
     const int64_t row = v ? j - tokens : j;
     const int64_t r = row / n;
-    quantize_row<F16, QMAX, D>(v ? Xv : Xk, v ? Qv : Qk, v ? Sv : Sk, row, r * cap + pos + (row - r * n),
-                               j < 2 * tokens, i);
+    int64_t p = pos;
+    bool fits = true;
+    if (pos_of && in) {
+      p = pos_of[r / rows_per_pos];
+      fits = p >= 0 && p <= cap - n;
+    }
+    quantize_row<F16, QMAX, D>(v ? Xv : Xk, v ? Qv : Qk, v ? Sv : Sk, row, r * cap + (fits ? p : 0) + (row - r * n),
+                               in && fits, i);
   }
 }
 
@@ -212,15 +223,18 @@ hipError_t launch_q(int D, const void* X, void* Q, void* S, int64_t tokens, hipS
 
 template <bool F16, int QMAX>
 hipError_t launch_qa(int D, const void* Xk, const void* Xv, void* Qk, void* Qv, void* Sk, void* Sv, int64_t tokens,
-                     int64_t n, int64_t cap, int64_t pos, hipStream_t st) {
+                     int64_t n, int64_t cap, int64_t pos, const int32_t* pos_of, int64_t rows_per_pos,
+                     hipStream_t st) {
   const int64_t want = (2 * tokens + 15) / 16;
   const unsigned grid = (unsigned)(want < (1 << 16) ? want : (1 << 16));
   if (D == 128)
     hipLaunchKernelGGL((quantize_append_kernel<F16, QMAX, 128>), dim3(grid), dim3(256), 0, st, Xk, Xv,
-                       (uint8_t*)Qk, (uint8_t*)Qv, (_Float16*)Sk, (_Float16*)Sv, tokens, n, cap, pos);
+                       (uint8_t*)Qk, (uint8_t*)Qv, (_Float16*)Sk, (_Float16*)Sv, tokens, n, cap, pos, pos_of,
+                       rows_per_pos);
   else
     hipLaunchKernelGGL((quantize_append_kernel<F16, QMAX, 64>), dim3(grid), dim3(256), 0, st, Xk, Xv,
-                       (uint8_t*)Qk, (uint8_t*)Qv, (_Float16*)Sk, (_Float16*)Sv, tokens, n, cap, pos);
+                       (uint8_t*)Qk, (uint8_t*)Qv, (_Float16*)Sk, (_Float16*)Sv, tokens, n, cap, pos, pos_of,
+                       rows_per_pos);
   return hipGetLastError();
 }
 
@@ -228,15 +242,17 @@ hipError_t launch_qa(int D, const void* Xk, const void* Xv, void* Qk, void* Qv, 
 
 hipError_t launch_quantize_append(int src_f16, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,
                                   void* Sk, void* Sv, int64_t rows, int64_t n, int64_t cap, int64_t pos,
-                                  hipStream_t st) {
-  if (rows < 1 || n < 1 || cap < 1 || pos < 0 || pos + n > cap || (D != 64 && D != 128)) return hipErrorInvalidValue;
+                                  const int32_t* pos_of, int64_t rows_per_pos, hipStream_t st) {
+  if (rows < 1 || n < 1 || cap < 1 || n > cap || (D != 64 && D != 128)) return hipErrorInvalidValue;
+  if (pos_of ? (rows_per_pos < 1 || rows % rows_per_pos != 0) : (pos < 0 || pos + n > cap))
+    return hipErrorInvalidValue;
   const int64_t tokens = rows * n;
   if (fmt == KV_I8)
-    return src_f16 ? launch_qa<true, 127>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, st)
-                   : launch_qa<false, 127>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, st);
+    return src_f16 ? launch_qa<true, 127>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st)
+                   : launch_qa<false, 127>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st);
   if (fmt == KV_I4)
-    return src_f16 ? launch_qa<true, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, st)
-                   : launch_qa<false, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, st);
+    return src_f16 ? launch_qa<true, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st)
+                   : launch_qa<false, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st);
   return hipErrorInvalidValue;
 }
 

@@ -562,6 +562,41 @@ static void quantize_kv_append(torch::Tensor Kn, torch::Tensor Vn, torch::Tensor
            "launch");
 }
 
+// quantize_kv_append_at_(K_new[B,H,n,D], V_new, K_cache[B,H,cap,D or D/2], V_cache, Ks_cache[B,H,cap],
+// Vs_cache, pos[B] int32) -> None: as quantize_kv_append_, sequence b's new tokens at positions
+// pos[b] .. pos[b]+n-1, read on the device (graph-capturable); out-of-range rows are not written.
+static void quantize_kv_append_at(torch::Tensor Kn, torch::Tensor Vn, torch::Tensor Kc, torch::Tensor Vc,
+                                  torch::Tensor Ksc, torch::Tensor Vsc, torch::Tensor pos) {
+  check_gpu({&Kn, &Vn, &Kc, &Vc, &Ksc, &Vsc, &pos});
+  TORCH_CHECK(Kn.scalar_type() == torch::kHalf || Kn.scalar_type() == torch::kFloat,
+              "fp16: K_new must be float16 or float32");
+  TORCH_CHECK(Vn.scalar_type() == Kn.scalar_type() && Vn.sizes() == Kn.sizes() && Kn.dim() == 4,
+              "shape: K_new and V_new must be [B,H,n,D] of one dtype; got ", Kn.sizes(), " and ", Vn.sizes());
+  TORCH_CHECK(Kc.scalar_type() == torch::kChar || Kc.scalar_type() == torch::kByte,
+              "int8: caches must be int8 or packed uint8 (int4)");
+  const int fmt = Kc.scalar_type() == torch::kChar ? FQKV_KV_I8 : FQKV_KV_I4;
+  const int64_t B = Kn.size(0), H = Kn.size(1), n = Kn.size(2), D = Kn.size(3);
+  check_D(D);
+  TORCH_CHECK(Kc.dim() == 4 && Kc.size(0) == B && Kc.size(1) == H && Kc.size(3) == (fmt == FQKV_KV_I8 ? D : D / 2) &&
+                  Vc.sizes() == Kc.sizes() && Vc.scalar_type() == Kc.scalar_type(),
+              "shape: caches must be [B,H,capacity,", fmt == FQKV_KV_I8 ? "D" : "D/2", "] matching K_new ", Kn.sizes(),
+              "; got ", Kc.sizes(), " and ", Vc.sizes());
+  const int64_t cap = Kc.size(2);
+  check_half(Ksc, "Ks_cache");
+  check_half(Vsc, "Vs_cache");
+  TORCH_CHECK(Ksc.sizes() == at::IntArrayRef({B, H, cap}) && Vsc.sizes() == Ksc.sizes(),
+              "shape: scale caches must be [B,H,capacity] = [", B, ",", H, ",", cap, "]; got ", Ksc.sizes(), " and ",
+              Vsc.sizes());
+  TORCH_CHECK(pos.scalar_type() == torch::kInt && pos.dim() == 1 && pos.size(0) == B && pos.is_contiguous(),
+              "shape: pos must be int32 [B] = [", B, "], contiguous");
+  const c10::DeviceGuard guard(Kn.device());
+  check_rc(fqkv_quantize_kv_append_at(Kn.data_ptr(), Vn.data_ptr(),
+                                      Kn.scalar_type() == torch::kHalf ? FQKV_SRC_F16 : FQKV_SRC_F32, Kc.data_ptr(),
+                                      Vc.data_ptr(), Ksc.data_ptr(), Vsc.data_ptr(), B * H, n, cap,
+                                      pos.data_ptr<int32_t>(), H, D, fmt, cur_stream(Kn)),
+           "launch");
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "MI355X fused single-query decode attention (fp16 / int8-KV / int4-KV / GQA / GQA split-K)";
   m.def("decode_attn_fp16_mw", &decode_attn_fp16_mw, "fp16 fused decode", py::arg("q"), py::arg("K"), py::arg("V"),
@@ -611,6 +646,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "per-token int4 KV quantizer on the GPU -> (packed uint8 [..., D/2], fp16 scales [...])", py::arg("X"));
   m.def("quantize_kv_append_", &quantize_kv_append,
         "quantize new K/V tokens [B,H,n,D] into int8 / int4 caches [B,H,capacity,.] at position pos, in place",
+        py::arg("K_new"), py::arg("V_new"), py::arg("K_cache"), py::arg("V_cache"), py::arg("Ks_cache"),
+        py::arg("Vs_cache"), py::arg("pos"));
+  m.def("quantize_kv_append_at_", &quantize_kv_append_at,
+        "quantize_kv_append_ with each sequence's position read on the device from pos [B] int32 (graph-capturable)",
         py::arg("K_new"), py::arg("V_new"), py::arg("K_cache"), py::arg("V_cache"), py::arg("Ks_cache"),
         py::arg("Vs_cache"), py::arg("pos"));
   m.def("_choose_splits", &choose_splits, "split count the single-block entry points use");

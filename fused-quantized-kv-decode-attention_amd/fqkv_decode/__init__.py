@@ -21,6 +21,9 @@ Beyond the reference (same conventions, no counterpart there):
     quantize_kv_append_(K_new[B,H,n,D], V_new, K_cache[B,H,cap,D or D/2], V_cache,
         Ks_cache[B,H,cap], Vs_cache, pos) -> None  the quantizers in append form for a live
                                                     cache: one launch, in place at pos
+    quantize_kv_append_at_(K_new, V_new, K_cache, V_cache, Ks_cache, Vs_cache, pos[B] int32)
+                                                    the same with each sequence's position read
+                                                    on the device (graph-capturable)
     decode_attn_gqa_nhd(q[B,Hq,D], K[B,N,Hkv,D], V, W, Ks=None, Vs=None) -> o[B,Hq,D]
                                                     token-major (FlashInfer NHD) KV layout
     decode_attn_gqa_strided(q[B,Hq,D], K[B,Hkv,N,D] view, V, W, Ks=None, Vs=None) -> o[B,Hq,D]
@@ -59,6 +62,7 @@ __all__ = [
     "quantize_int8_per_token",
     "quantize_int4_per_token",
     "quantize_kv_append_",
+    "quantize_kv_append_at_",
     "decode_attn_gqa_nhd",
     "decode_attn_gqa_strided",
     "decode_attn_gqa_paged",
@@ -70,7 +74,7 @@ __all__ = [
 _ENTRY_POINTS = ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa",
                  "gqa_sk_fast", "decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8",
                  "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token", "quantize_kv_append_",
-                 "decode_attn_gqa_nhd", "decode_attn_gqa_strided", "decode_attn_gqa_paged")
+                 "quantize_kv_append_at_", "decode_attn_gqa_nhd", "decode_attn_gqa_strided", "decode_attn_gqa_paged")
 _EXT = None
 
 

@@ -96,24 +96,33 @@ def attention_forward(module, query, key, value, attention_mask=None, scaling=No
 
 
 def _static_attention(module, query, key, value, attention_mask, scaling, dropout, **kwargs):
-    """Attention over a StaticKVCache layer's whole buffers [B, Hkv, capacity, D]: a decode step runs the
-    paged kernel over the first seq_lens[b] tokens of sequence b's buffer (one page of ``capacity``
-    tokens; the lengths are read on the device); anything else goes to SDPA with transformers' mask."""
+    """Attention over a StaticKVCache layer's whole buffers [B, Hkv, capacity, D] (fp16, or int8 /
+    packed int4 carrying their fp16 scales [B, Hkv, capacity]): a decode step runs the paged kernel
+    over the first seq_lens[b] tokens of sequence b's buffer (one page of ``capacity`` tokens; the
+    lengths are read on the device); anything else goes to SDPA with transformers' mask (over the
+    dequantized cache for int8 / int4)."""
     B, Hq, qlen, D = query.shape
+    ks, vs = getattr(key, "fqkv_scales", None), getattr(value, "fqkv_scales", None)
     # a caller's padding mask (folded into transformers' mask by the builder register() installs)
     # may hide positions below the length: that step goes to SDPA with the mask
     ok = (qlen == 1 and not dropout and not getattr(module, "training", False) and query.is_cuda
           and not getattr(attention_mask, "fqkv_padding", False)
-          and key.dtype == torch.float16 and D in (64, 128) and Hq % key.shape[1] == 0
+          and (key.dtype == torch.float16 or ks is not None) and D in (64, 128) and Hq % key.shape[1] == 0
           and kwargs.get("sliding_window") is None and kwargs.get("softcap") is None
           and (scaling is None or abs(scaling * math.sqrt(D) - 1.0) <= 1e-6))
     if not ok:
+        if ks is not None:
+            from . import quant
+
+            deq = quant.dequant_int8 if key.dtype == torch.int8 else quant.dequant_int4
+            key, value = deq(key, ks).to(query.dtype), deq(value, vs).to(query.dtype)
         return _sdpa(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
     from . import decode_attn_gqa_paged
 
     q = query[:, :, 0, :].to(torch.float16).contiguous()
+    pages = lambda t: None if t is None else t.permute(0, 2, 1)  # [B, Hkv, cap] -> [B, cap, Hkv]
     out = decode_attn_gqa_paged(q, key.permute(0, 2, 1, 3), value.permute(0, 2, 1, 3), key.fqkv_page_table,
-                                key.fqkv_seq_lens, key.shape[2], _W)
+                                key.fqkv_seq_lens, key.shape[2], _W, pages(ks), pages(vs))
     return out.unsqueeze(1).to(query.dtype), None
 
 
@@ -308,29 +317,97 @@ def _make_static_layer_class():
                 self.cumulative_length.zero_()
                 self.seq_lens.zero_()
 
-    return DeviceLengthStaticLayer
+    class DeviceLengthQuantizedLayer(DeviceLengthStaticLayer):
+        """The same with int8 (or packed int4) keys and values and fp16 per-token scales, new tokens
+        quantized into place at the position held on the device (``quantize_kv_append_at_``, bytes
+        equal to ``fqkv_decode.quant``'s quantizers). The first call (the prompt) attends to its exact
+        states, with a mask of their length; later calls get the quantized buffers, tagged with
+        their scales."""
+
+        def __init__(self, max_cache_len, kv_format):
+            if kv_format not in ("int8", "int4"):
+                raise ValueError("kv_format must be 'int8' or 'int4', got %r" % (kv_format,))
+            super().__init__(max_cache_len)
+            self.kv_format = kv_format
+            self.prefilled = False
+
+        def lazy_initialization(self, key_states, value_states):
+            self.dtype, self.device = key_states.dtype, key_states.device
+            self.batch_size, self.num_heads = key_states.shape[:2]
+            B, H, D = self.batch_size, self.num_heads, key_states.shape[-1]
+            self.k_head_dim = self.v_head_dim = D
+            width, dt = (D, torch.int8) if self.kv_format == "int8" else (D // 2, torch.uint8)
+            cap = self.max_cache_len
+            self.keys = torch.zeros(B, H, cap, width, dtype=dt, device=self.device)
+            self.values = torch.zeros_like(self.keys)
+            self.key_scales = torch.zeros(B, H, cap, dtype=torch.float16, device=self.device)
+            self.value_scales = torch.zeros_like(self.key_scales)
+            self.cumulative_length = self.cumulative_length.to(self.device)
+            self.seq_lens = torch.zeros(B, dtype=torch.int32, device=self.device)
+            self.page_table = torch.arange(B, dtype=torch.int32, device=self.device).view(B, 1)
+            for t, sc in ((self.keys, self.key_scales), (self.values, self.value_scales)):
+                t.fqkv_seq_lens = self.seq_lens
+                t.fqkv_page_table = self.page_table
+                t.fqkv_scales = sc
+            self.is_initialized = True
+
+        def update(self, key_states, value_states, *args, **kwargs):
+            from . import quantize_kv_append_at_
+
+            if not self.is_initialized:
+                self.lazy_initialization(key_states, value_states)
+            n = key_states.shape[-2]
+            kn, vn = key_states, value_states
+            if kn.dtype not in (torch.float16, torch.float32):
+                kn, vn = kn.float(), vn.float()
+            # one launch quantizes the new K and V tokens into their slots, at seq_lens on the device
+            quantize_kv_append_at_(kn.contiguous(), vn.contiguous(), self.keys, self.values, self.key_scales,
+                                   self.value_scales, self.seq_lens)
+            self.seq_lens.add_(n)
+            self.cumulative_length.add_(n)
+            if not self.prefilled:
+                self.prefilled = True
+                return key_states, value_states
+            return self.keys, self.values
+
+        def get_mask_sizes(self, query_length):
+            return (self.max_cache_len, 0) if self.prefilled else (query_length, 0)
+
+        def reset(self):
+            super().reset()
+            self.prefilled = False
+            if self.is_initialized:
+                self.key_scales.zero_()
+                self.value_scales.zero_()
+
+    return DeviceLengthStaticLayer, DeviceLengthQuantizedLayer
 
 
-_STATIC_LAYER_CLASS = None
+_STATIC_LAYER_CLASSES = None
 
 
-def StaticKVCache(config, max_cache_len):
+def StaticKVCache(config, max_cache_len, kv_format=None):
     """A transformers ``Cache`` of preallocated fp16 KV buffers with the sequence lengths on the
     device, for decode steps captured in a HIP graph (:func:`generate_graphed`). ``max_cache_len``
     (a power of two in [16, 2^20]) bounds prompt plus generated tokens. Decode steps on the kernel
     attend to the first ``length`` positions of each buffer and read no attention mask, so a call
     that passes a padding mask runs its decode steps on SDPA instead (still correct, not
-    graph-replayed by :func:`generate_graphed`, which passes none)."""
+    graph-replayed by :func:`generate_graphed`, which passes none). ``kv_format`` "int8" or "int4"
+    stores the cache in that per-token format, quantized on the GPU as tokens arrive (the prompt
+    attends to its exact states, later calls to the quantized cache)."""
     from transformers.cache_utils import Cache
 
-    global _STATIC_LAYER_CLASS
-    if _STATIC_LAYER_CLASS is None:
-        _STATIC_LAYER_CLASS = _make_static_layer_class()
+    global _STATIC_LAYER_CLASSES
+    if _STATIC_LAYER_CLASSES is None:
+        _STATIC_LAYER_CLASSES = _make_static_layer_class()
+    fp16_layer, quant_layer = _STATIC_LAYER_CLASSES
     text = config.get_text_config(decoder=True) if hasattr(config, "get_text_config") else config
-    return Cache(layers=[_STATIC_LAYER_CLASS(max_cache_len) for _ in range(text.num_hidden_layers)])
+    if kv_format is None:
+        return Cache(layers=[fp16_layer(max_cache_len) for _ in range(text.num_hidden_layers)])
+    return Cache(layers=[quant_layer(max_cache_len, kv_format) for _ in range(text.num_hidden_layers)])
 
 
-def generate_graphed(model, input_ids, max_new_tokens, max_cache_len=None, use_graph=True):
+def generate_graphed(model, input_ids, max_new_tokens, max_cache_len=None, use_graph=True, kv_format=None):
     """Greedy decoding with every decode step replayed from one captured HIP graph.
 
     The prompt runs eagerly into a :func:`StaticKVCache` (capacity ``max_cache_len``, by default the
@@ -340,7 +417,8 @@ def generate_graphed(model, input_ids, max_new_tokens, max_cache_len=None, use_g
     the paged kernel when the model's attention implementation is this module's), and writes its
     argmax back as the next step's input. The prompt rows are taken as unpadded (no attention mask
     is passed).
-    ``use_graph=False`` runs the same steps eagerly. Returns the new tokens, [B, max_new_tokens]."""
+    ``use_graph=False`` runs the same steps eagerly; ``kv_format`` "int8" / "int4" keeps the cache in
+    that format (:func:`StaticKVCache`). Returns the new tokens, [B, max_new_tokens]."""
     B, L = input_ids.shape
     if max_new_tokens < 1:
         raise ValueError("max_new_tokens must be >= 1")
@@ -348,7 +426,7 @@ def generate_graphed(model, input_ids, max_new_tokens, max_cache_len=None, use_g
     if L + max_new_tokens > cap:
         raise ValueError("prompt + new tokens (%d) exceed max_cache_len (%d)" % (L + max_new_tokens, cap))
     dev = input_ids.device
-    cache = StaticKVCache(model.config, cap)
+    cache = StaticKVCache(model.config, cap, kv_format)
     out = torch.empty(B, max_new_tokens, dtype=torch.long, device=dev)
     with torch.no_grad():
         logits = model(input_ids, past_key_values=cache, use_cache=True).logits

@@ -287,6 +287,19 @@ int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, v
                             int64_t pos, int64_t D, int kv_format, void* stream);
 
 /*
+ * fqkv_quantize_kv_append with the positions on the device: the new tokens of
+ * cache row r go to positions pos[r / rows_per_pos] .. + n_new - 1, read by the
+ * kernel (pos: int32, rows / rows_per_pos entries, e.g. one per sequence with
+ * rows_per_pos = KV heads), so a captured graph appends wherever the cache
+ * ends at replay time. Rows whose tokens would leave [0, capacity) are not
+ * written. No counterpart in the reference; for decode loops replayed from
+ * HIP graphs over a preallocated int8 / int4 cache.
+ */
+int fqkv_quantize_kv_append_at(const void* K_new, const void* V_new, int x_dtype, void* K_cache, void* V_cache,
+                               void* Ks_cache, void* Vs_cache, int64_t rows, int64_t n_new, int64_t capacity,
+                               const int32_t* pos, int64_t rows_per_pos, int64_t D, int kv_format, void* stream);
+
+/*
  * Split merge mode for calls that split the sequence (gqa_sk_fast with S > 1
  * and the internal splits of the single-block entry points). Default (0):
  * one kernel per call; the last workgroup of each head group to finish merges

@@ -155,6 +155,23 @@ def test_capi_quantize_append_rejects_bad_args(lib):
     assert f(16, 16, 1, 20, 16, 16, 16, 8, 1, 100, 0, 128, 1, None) == 1 and "aligned" in _err(lib)
 
 
+def test_capi_quantize_append_at_rejects_bad_args(lib):
+    """The device-position append: positions are read on the GPU, so the host checks the rest
+    (n_new fits the capacity, rows_per_pos divides rows, pointers and their alignment)."""
+    f = lib.fqkv_quantize_kv_append_at
+    f.argtypes = [VP, VP, ctypes.c_int] + [VP] * 4 + [I64] * 3 + [VP, I64, I64, ctypes.c_int, VP]
+    ok = [16, 16, 1, 16, 16, 16, 16]
+    assert f(*ok, 8, 101, 100, 16, 4, 128, 1, None) == 1 and _err(lib).startswith("pos:")
+    assert f(*ok, 8, 1, 100, 16, 3, 128, 1, None) == 1 and "rows_per_pos" in _err(lib)
+    assert f(*ok, 8, 1, 100, 16, 0, 128, 1, None) == 1 and "rows_per_pos" in _err(lib)
+    assert f(*ok, 8, 1, 100, None, 4, 128, 1, None) == 1 and "null" in _err(lib)
+    assert f(*ok, 8, 1, 100, 18, 4, 128, 1, None) == 1 and "aligned" in _err(lib)
+    assert f(*ok, 8, 0, 100, 16, 4, 128, 1, None) == 1 and "n_new" in _err(lib)
+    assert f(*ok, 8, 1, 100, 16, 4, 128, 0, None) == 1 and "kv_format" in _err(lib)
+    assert f(*ok, 8, 1, 100, 16, 4, 96, 2, None) == 1 and _err(lib).startswith("D:")
+    assert f(16, 16, 2, 16, 16, 16, 16, 8, 1, 100, 16, 4, 128, 1, None) == 1 and "x_dtype" in _err(lib)
+
+
 def test_capi_quantized_gqa_and_split_reject_bad_args(lib):
     fg = lib.fqkv_decode_attn_gqa_quant
     fg.argtypes = [VP] * 6 + [I64] * 5 + [ctypes.c_int, I64, VP, ctypes.c_size_t, VP]

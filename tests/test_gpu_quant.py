@@ -134,6 +134,63 @@ def test_gpu_quantize_append_writes_only_its_slots(dtype, D, fmt):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_gpu_quantize_append_at_device_positions(dtype, D, fmt):
+    """quantize_kv_append_at_ writes sequence b's new tokens at pos[b] (an int32 tensor read on the
+    GPU): the caches equal quantize_kv_append_ called per sequence at that position. Sequences whose
+    tokens would not fit in [0, capacity) (pos < 0, pos + n > capacity) are left untouched, and the
+    same call replayed from a captured graph follows the positions as they change."""
+    B, H, cap = 5, 3, 40
+    g = torch.Generator().manual_seed(64)
+    width, qdt = (D, torch.int8) if fmt == "int8" else (D // 2, torch.uint8)
+
+    def caches():
+        Kc = torch.full((B, H, cap, width), 0x55, dtype=qdt, device="cuda")
+        Ksc = torch.full((B, H, cap), 7.0, dtype=torch.float16, device="cuda")
+        return [Kc, torch.full_like(Kc, 0x33), Ksc, torch.full_like(Ksc, 9.0)]
+
+    for n, positions in ((4, [0, 7, 36, 37, -1]), (1, [39, 0, 40, 12, -7]), (17, [23, 3, 24, 0, 2**31 - 1])):
+        Kn = (torch.randn(B, H, n, D, generator=g) * 3).to(dtype).cuda()
+        Vn = (torch.randn(B, H, n, D, generator=g) * 3).to(dtype).cuda()
+        got, want = caches(), caches()
+        pos = torch.tensor(positions, dtype=torch.int32, device="cuda")
+        fq.quantize_kv_append_at_(Kn, Vn, *got, pos)
+        for b, p in enumerate(positions):
+            if 0 <= p <= cap - n:
+                per_seq = [t[b:b + 1] for t in want]
+                fq.quantize_kv_append_(Kn[b:b + 1].contiguous(), Vn[b:b + 1].contiguous(), *per_seq, p)
+        for x, y in zip(got, want):
+            assert torch.equal(x, y)
+
+    # captured: each replay appends one token where pos points, then the graph-free add moves pos on
+    Kn = (torch.randn(B, H, 1, D, generator=g) * 3).to(dtype).cuda()
+    Vn = (torch.randn(B, H, 1, D, generator=g) * 3).to(dtype).cuda()
+    got, want = caches(), caches()
+    pos = torch.tensor([0, 5, 10, 38, 39], dtype=torch.int32, device="cuda")
+    start = pos.clone()
+    fq.quantize_kv_append_at_(Kn, Vn, *got, pos)  # first call outside the capture loads the kernel
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fq.quantize_kv_append_at_(Kn, Vn, *got, pos)
+    for step in range(3):
+        pos.copy_(start + step)
+        graph.replay()
+        torch.cuda.synchronize()
+    for step in range(3):
+        for b, p in enumerate((start + step).tolist()):
+            if p <= cap - 1:
+                fq.quantize_kv_append_(Kn[b:b + 1].contiguous(), Vn[b:b + 1].contiguous(), *[t[b:b + 1] for t in want],
+                                       p)
+    for x, y in zip(got, want):
+        assert torch.equal(x, y)
+    with pytest.raises(RuntimeError, match="^shape: pos"):
+        fq.quantize_kv_append_at_(Kn, Vn, *got, pos[:4])
+    with pytest.raises(RuntimeError, match="^shape: pos"):
+        fq.quantize_kv_append_at_(Kn, Vn, *got, pos.long())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("fmt", ["int8", "int4"])
 def test_reference_quantizer_expressions_on_gpu_match_oracle(dtype, fmt):
     """The reference quantizes with PyTorch expressions on its device tensors,
