@@ -43,6 +43,11 @@ step to the next and :func:`generate_graphed` captures one whole step of the
 model in a HIP graph and replays it per token::
 
     tokens = hf_llama.generate_graphed(model, ids, max_new_tokens=128)
+
+With ``kv_format="int8"`` or ``"int4"`` (on both) the static cache stores that
+per-token format; each step quantizes its new token into place with
+``quantize_kv_append_at_``, which reads the position from the device, so the
+quantized cache is graph-replayed too.
 """
 
 import math
@@ -317,6 +322,22 @@ def _make_static_layer_class():
                 self.cumulative_length.zero_()
                 self.seq_lens.zero_()
 
+        def _state(self):
+            return (self.keys, self.values, self.seq_lens)
+
+        def reorder_cache(self, beam_idx):
+            # in place, so the buffers keep their tags and the addresses a captured graph holds
+            if self.is_initialized:
+                idx = beam_idx.to(self.device)
+                for t in self._state():
+                    t.copy_(t.index_select(0, idx))
+
+        def offload(self):
+            raise NotImplementedError("StaticKVCache layers stay on their GPU (the lengths live there)")
+
+        def prefetch(self):
+            raise NotImplementedError("StaticKVCache layers stay on their GPU (the lengths live there)")
+
     class DeviceLengthQuantizedLayer(DeviceLengthStaticLayer):
         """The same with int8 (or packed int4) keys and values and fp16 per-token scales, new tokens
         quantized into place at the position held on the device (``quantize_kv_append_at_``, bytes
@@ -372,6 +393,9 @@ def _make_static_layer_class():
 
         def get_mask_sizes(self, query_length):
             return (self.max_cache_len, 0) if self.prefilled else (query_length, 0)
+
+        def _state(self):
+            return (self.keys, self.values, self.key_scales, self.value_scales, self.seq_lens)
 
         def reset(self):
             super().reset()

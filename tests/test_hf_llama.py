@@ -285,6 +285,26 @@ def test_static_cache_cpu_decode_matches_dynamic_cache():
     assert cache.layers[0].seq_lens.tolist() == [17, 17]
 
 
+def test_static_cache_reorders_in_place():
+    """reorder_cache (beam search) on the static cache permutes the buffers and lengths in place,
+    so they keep the tags the attention function reads and the addresses a graph captured."""
+    model = tiny_llama(layers=2, hidden=256, heads=4, kv_heads=2)
+    set_impl(model, hf_llama.register())
+    ids = torch.randint(0, 1000, (3, 10), generator=torch.Generator().manual_seed(9))
+    cache = hf_llama.StaticKVCache(model.config, 16)
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+    layer = cache.layers[0]
+    layer.seq_lens.copy_(torch.tensor([10, 9, 8], dtype=torch.int32))
+    keys, ptr, before = layer.keys, layer.keys.data_ptr(), layer.keys.clone()
+    cache.reorder_cache(torch.tensor([2, 2, 0]))
+    assert layer.keys is keys and layer.keys.data_ptr() == ptr and keys.fqkv_seq_lens is layer.seq_lens
+    assert torch.equal(layer.keys, before[[2, 2, 0]])
+    assert layer.seq_lens.tolist() == [8, 8, 10]
+    with pytest.raises(NotImplementedError):
+        layer.offload()
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("geometry", sorted(GEOMETRIES))
 def test_gpu_graphed_generation(geometry, monkeypatch):
@@ -414,6 +434,29 @@ def test_gpu_static_quantized_cache_prefill_and_decode(fmt):
     ref = torch.softmax(q.float() @ Kf.transpose(-1, -2).contiguous() / 8, -1) @ Vf
     err = float((o.float().transpose(1, 2) - ref).abs().max())
     assert err <= 2e-3 * max(1.0, float(ref.abs().max())), (err, float(ref.abs().max()))
+
+
+@pytest.mark.gpu
+def test_gpu_static_quantized_cache_reorders_scales_and_lengths():
+    """Beam-search reordering of an int4 static cache moves the scales and lengths with the bytes:
+    after reorder_cache([1, 1]) a decode step of the same token gives both rows the logits row 1
+    gets without the reorder, bit for bit."""
+    name = hf_llama.register()
+    model = tiny_llama(layers=2, dtype=torch.float16, device="cuda")
+    set_impl(model, name)
+    ids = torch.randint(0, 1000, (2, 40), generator=torch.Generator().manual_seed(10)).cuda()
+    tok = torch.randint(0, 1000, (2, 1), generator=torch.Generator().manual_seed(11)).cuda()
+    pos = torch.full((2, 1), 40, dtype=torch.long, device="cuda")
+    out = []
+    for reorder in (False, True):
+        cache = hf_llama.StaticKVCache(model.config, 64, "int4")
+        with torch.no_grad():
+            model(ids, past_key_values=cache, use_cache=True)
+            if reorder:
+                cache.reorder_cache(torch.tensor([1, 1]))
+            out.append(model(tok[[1, 1]] if reorder else tok, past_key_values=cache, position_ids=pos,
+                             use_cache=True).logits)
+    assert torch.equal(out[1][0], out[0][1]) and torch.equal(out[1][1], out[0][1])
 
 
 @pytest.mark.gpu
