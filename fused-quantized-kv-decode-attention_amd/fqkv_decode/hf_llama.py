@@ -301,6 +301,15 @@ def _make_static_layer_class():
                                  "sequence), got %r" % (max_cache_len,))
             super().__init__(max_cache_len=max_cache_len)
             self.seq_lens = self.page_table = None
+            self.tokens = 0  # tokens stored, counted on the host (graph replays do not come through here)
+
+        def _count(self, n):
+            # checked before anything is written: the kernels would clamp the lengths, so a cache that
+            # overflowed would attend to its first max_cache_len tokens without a word
+            if self.tokens + n > self.max_cache_len:
+                raise ValueError("StaticKVCache: %d cached + %d new tokens exceed max_cache_len %d"
+                                 % (self.tokens, n, self.max_cache_len))
+            self.tokens += n
 
         def lazy_initialization(self, key_states, value_states):
             super().lazy_initialization(key_states, value_states)
@@ -312,12 +321,14 @@ def _make_static_layer_class():
                 t.fqkv_page_table = self.page_table
 
         def update(self, key_states, value_states, *args, **kwargs):
+            self._count(key_states.shape[-2])
             keys, values = super().update(key_states, value_states, *args, **kwargs)
             self.seq_lens.add_(key_states.shape[-2])
             return keys, values
 
         def reset(self):
             super().reset()
+            self.tokens = 0
             if self.is_initialized:
                 self.cumulative_length.zero_()
                 self.seq_lens.zero_()
@@ -375,9 +386,10 @@ def _make_static_layer_class():
         def update(self, key_states, value_states, *args, **kwargs):
             from . import quantize_kv_append_at_
 
+            n = key_states.shape[-2]
+            self._count(n)
             if not self.is_initialized:
                 self.lazy_initialization(key_states, value_states)
-            n = key_states.shape[-2]
             kn, vn = key_states, value_states
             if kn.dtype not in (torch.float16, torch.float32):
                 kn, vn = kn.float(), vn.float()

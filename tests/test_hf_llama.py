@@ -285,6 +285,27 @@ def test_static_cache_cpu_decode_matches_dynamic_cache():
     assert cache.layers[0].seq_lens.tolist() == [17, 17]
 
 
+def test_static_cache_refuses_to_overflow():
+    """More tokens than max_cache_len raise before anything is written (the kernels would clamp
+    the lengths and attend to the first max_cache_len tokens), for the fp16 and the int8 layer."""
+    model = tiny_llama(layers=2, hidden=256, heads=4, kv_heads=2)
+    set_impl(model, hf_llama.register())
+    cache = hf_llama.StaticKVCache(model.config, 16)
+    ids = torch.randint(0, 1000, (1, 14), generator=torch.Generator().manual_seed(12))
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+        model(ids[:, :2], past_key_values=cache, position_ids=torch.tensor([[14, 15]]), use_cache=True)
+        with pytest.raises(ValueError, match="exceed max_cache_len 16"):
+            model(ids[:, :1], past_key_values=cache, position_ids=torch.tensor([[16]]), use_cache=True)
+    assert cache.layers[0].seq_lens.tolist() == [16]
+    cache.reset()
+    assert cache.layers[0].tokens == 0 and cache.layers[0].seq_lens.tolist() == [0]
+    layer = hf_llama.StaticKVCache(model.config, 16, "int8").layers[0]
+    with pytest.raises(ValueError, match="exceed max_cache_len"):
+        layer.update(torch.zeros(1, 2, 17, 64), torch.zeros(1, 2, 17, 64))
+    assert not layer.is_initialized
+
+
 def test_static_cache_reorders_in_place():
     """reorder_cache (beam search) on the static cache permutes the buffers and lengths in place,
     so they keep the tags the attention function reads and the addresses a graph captured."""
