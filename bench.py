@@ -738,6 +738,35 @@ def suite_quant(torch, fq, steps, warmup, rows):
             log("quantizer %s from %s: %8.2f us  %7.1f GB/s" % (fmt, src, ms * 1e3, nbytes / ms / 1e6))
         del X
     del X32
+    # the paged writer at a serving shape: a 16384-token batch of new fp16 K and V rows (Hkv 8,
+    # D 128) into shuffled head-major pages of 16 tokens (4096 pages), every slot written once;
+    # bytes: the fp16 rows read, the codes and scales written, the slot ids read
+    T, H, P, page = 16384, 8, 4096, 16
+    Kn = torch.randn(T, H, Dd, device="cuda", generator=g).half()
+    Vn = torch.randn(T, H, Dd, device="cuda", generator=g).half()
+    slots = torch.randperm(P * page, device="cuda", generator=g)[:T].to(torch.int32)
+    for fmt in ("int8", "int4"):
+        width, qdt = (Dd, torch.int8) if fmt == "int8" else (Dd // 2, torch.uint8)
+        Kp = torch.zeros(P, H, page, width, dtype=qdt, device="cuda").permute(0, 2, 1, 3)
+        Vp = torch.zeros(P, H, page, width, dtype=qdt, device="cuda").permute(0, 2, 1, 3)
+        Ks = torch.zeros(P, H, page, dtype=torch.float16, device="cuda").permute(0, 2, 1)
+        Vs = torch.zeros(P, H, page, dtype=torch.float16, device="cuda").permute(0, 2, 1)
+        fq.quantize_kv_to_pages_(Kn, Vn, slots, Kp, Vp, Ks, Vs)
+        f = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+        q, s = f(Kn)
+        pg, off = (slots // page).long(), (slots % page).long()
+        same = bool(torch.equal(Kp[pg, off], q) and torch.equal(Ks[pg, off], s))
+        if not same:
+            log("paged quantizer %s: bytes differ from quantize_%s_per_token" % (fmt, fmt))
+            continue
+        nbytes = 2 * (T * H * Dd * 2 + T * H * (width + 2)) + 4 * T
+        ms = _loop_ms(torch, lambda i: fq.quantize_kv_to_pages_(Kn, Vn, slots, Kp, Vp, Ks, Vs), 1,
+                      max(50, steps // 4), max(10, warmup // 4))
+        rows.append(_row("quantize_kv_to_pages_" + fmt, {"tokens": T, "Hkv": H, "D": Dd, "page": page, "pages": P,
+                                                        "layout": "HND", "src": "fp16"}, ms, nbytes,
+                         equal_to_quantizer=same))
+        log("paged quantizer %s (K+V, %d tokens): %8.2f us  %7.1f GB/s" % (fmt, T, ms * 1e3, nbytes / ms / 1e6))
+        del Kp, Vp, Ks, Vs
     torch.cuda.empty_cache()
 
 

@@ -719,4 +719,44 @@ int fqkv_quantize_kv_append_at(const void* K_new, const void* V_new, int x_dtype
   return FQKV_OK;
 }
 
+int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, const int32_t* slot_mapping,
+                           int64_t tokens, int64_t kv_heads, int64_t D, void* K_pages, void* V_pages,
+                           void* Ks_pages, void* Vs_pages, int64_t num_pages, int64_t page_size,
+                           int64_t page_stride, int64_t token_stride, int64_t head_stride, int64_t s_page_stride,
+                           int64_t s_token_stride, int64_t s_head_stride, int kv_format, void* stream) {
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32)
+    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16 or FQKV_SRC_F32");
+  if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
+  if (tokens < 0 || kv_heads < 1)
+    return fail(FQKV_ERR_ARG, "shape: tokens must be >= 0 and kv_heads >= 1, got %lld and %lld", (long long)tokens,
+                (long long)kv_heads);
+  if (num_pages < 1 || page_size < 1 || (page_size & (page_size - 1)) || page_size > (1 << 30))
+    return fail(FQKV_ERR_ARG, "page: num_pages must be >= 1 and page_size a power of two, got %lld and %lld",
+                (long long)num_pages, (long long)page_size);
+  const int64_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
+  if (page_stride < 0 || token_stride < 0 || head_stride < 0 || page_stride % qal || token_stride % qal ||
+      head_stride % qal)
+    return fail(FQKV_ERR_ARG, "stride: code strides must be non-negative multiples of %lld bytes", (long long)qal);
+  if (s_page_stride < 0 || s_token_stride < 0 || s_head_stride < 0)
+    return fail(FQKV_ERR_ARG, "stride: scale strides must be non-negative");
+  if (!K_new || !V_new || !slot_mapping || !K_pages || !V_pages || !Ks_pages || !Vs_pages)
+    return fail(FQKV_ERR_ARG, "null tensor pointer");
+  const uintptr_t xal = (x_dtype == FQKV_SRC_F16 && D == 64) ? 8 : 16;
+  if (!aligned(K_new, xal) || !aligned(V_new, xal)) return fail(FQKV_ERR_ARG, "K_new and V_new must be %d-byte aligned", (int)xal);
+  if (!aligned(K_pages, (uintptr_t)qal) || !aligned(V_pages, (uintptr_t)qal))
+    return fail(FQKV_ERR_ARG, "pages must be %d-byte aligned", (int)qal);
+  if (!aligned(Ks_pages, 2) || !aligned(Vs_pages, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
+  if (!aligned(slot_mapping, 4)) return fail(FQKV_ERR_ARG, "slot_mapping must be 4-byte aligned");
+  if (tokens == 0) return FQKV_OK;
+  const int page_log2 = __builtin_ctzll((unsigned long long)page_size);
+  hipError_t e = launch_quantize_pages(x_dtype == FQKV_SRC_F16, kv_format, (int)D, K_new, V_new, slot_mapping, tokens,
+                                       kv_heads, K_pages, V_pages, Ks_pages, Vs_pages, num_pages, page_log2,
+                                       page_stride, token_stride, head_stride, s_page_stride, s_token_stride,
+                                       s_head_stride, (hipStream_t)stream);
+  if (e != hipSuccess) return hip_fail(e, "launch: quantize pages kernel");
+  return FQKV_OK;
+}
+
 }  // extern "C"

@@ -119,5 +119,9 @@ hipError_t launch_quantize(int src_f16, int fmt, int D, const void* X, void* Q, 
 hipError_t launch_quantize_append(int src_f16, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,
                                   void* Sk, void* Sv, int64_t rows, int64_t n, int64_t cap, int64_t pos,
                                   const int32_t* pos_of, int64_t rows_per_pos, hipStream_t st);
+hipError_t launch_quantize_pages(int src_f16, int fmt, int D, const void* Xk, const void* Xv, const int32_t* slots,
+                                 int64_t tokens, int64_t heads, void* Qk, void* Qv, void* Sk, void* Sv,
+                                 int64_t num_pages, int page_log2, int64_t q_page, int64_t q_tok, int64_t q_head,
+                                 int64_t s_page, int64_t s_tok, int64_t s_head, hipStream_t st);
 
 }  // namespace fqkv

@@ -21,7 +21,8 @@
 //
 // Layout: 16 lanes own one token row (D/16 consecutive elements each); a wave
 // covers 4 rows per step, a 256-thread workgroup 16, grid-striding over rows.
-// The append form writes a live cache's new K and V tokens in place.
+// The append forms write a live cache's new K and V tokens in place, at host
+// or device positions of contiguous caches, or at slots of paged caches.
 // The row maximum is a DPP all-reduce within the 16-lane row. HBM-bound:
 // reads 2 or 4 B per element, writes 1 or 0.5 B per element + 2 B per row.
 #include <hip/hip_runtime.h>
@@ -82,13 +83,13 @@ __device__ __forceinline__ void load_row_slice(const void* X, int64_t row, int i
   }
 }
 
-// Quantize source row `row` of X into destination row `dst` of Q / scales.
-// The calling 16 lanes stay active together (the DPP reduction spans them);
-// a group with live == false reads and writes nothing.
+// Quantize source row `row` of X into the destination row at qrow (D int8
+// bytes or D/2 packed int4 bytes) and its scale at *srow. The calling 16
+// lanes stay active together (the DPP reduction spans them); a group with
+// live == false reads and writes nothing (its pointers may be anything).
 template <bool F16, int QMAX, int D>
-__device__ __forceinline__ void quantize_row(const void* __restrict__ X, uint8_t* __restrict__ Q,
-                                             _Float16* __restrict__ scales, int64_t row, int64_t dst, bool live,
-                                             int i) {
+__device__ __forceinline__ void quantize_row(const void* __restrict__ X, int64_t row, uint8_t* __restrict__ qrow,
+                                             _Float16* __restrict__ srow, bool live, int i) {
   constexpr int EPL = D / 16;  // elements per lane
   float x[EPL];
   if (live) {
@@ -145,7 +146,7 @@ __device__ __forceinline__ void quantize_row(const void* __restrict__ X, uint8_t
     for (int k = 0; k < EPL / 4; ++k)
       w[k] = (uint32_t)(q[4 * k] & 0xFF) | ((uint32_t)(q[4 * k + 1] & 0xFF) << 8) |
              ((uint32_t)(q[4 * k + 2] & 0xFF) << 16) | ((uint32_t)(q[4 * k + 3] & 0xFF) << 24);
-    uint8_t* out = Q + dst * D + EPL * i;
+    uint8_t* out = qrow + EPL * i;
     if constexpr (EPL == 8) {
       *(u2_t*)out = u2_t{w[0], w[1]};
     } else {
@@ -156,14 +157,20 @@ __device__ __forceinline__ void quantize_row(const void* __restrict__ X, uint8_t
 #pragma unroll
     for (int t = 0; t < EPL / 2; ++t)
       w |= ((uint32_t)(q[2 * t] & 0xF) | ((uint32_t)(q[2 * t + 1] & 0xF) << 4)) << (8 * t);
-    uint8_t* out = Q + dst * (D / 2) + (EPL / 2) * i;
+    uint8_t* out = qrow + (EPL / 2) * i;
     if constexpr (EPL == 8) {
       *(uint32_t*)out = w;
     } else {
       *(uint16_t*)out = (uint16_t)w;
     }
   }
-  if (i == 0) scales[dst] = s_out;
+  if (i == 0) *srow = s_out;
+}
+
+// Destination row dst of a contiguous [rows, D or D/2] code buffer.
+template <int QMAX, int D>
+__device__ __forceinline__ uint8_t* code_row(uint8_t* Q, int64_t dst) {
+  return Q + dst * (QMAX == 127 ? D : D / 2);
 }
 
 template <bool F16, int QMAX, int D>
@@ -173,7 +180,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(const void* __restrict__ 
   const int64_t rows_per_step = (int64_t)gridDim.x * (blockDim.x >> 4);
   for (int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
        row - (threadIdx.x >> 4) < tokens; row += rows_per_step)
-    quantize_row<F16, QMAX, D>(X, Q, scales, row, row, row < tokens, i);
+    quantize_row<F16, QMAX, D>(X, row, code_row<QMAX, D>(Q, row), scales + row, row < tokens, i);
 }
 
 // Append form for a live cache: K and V rows of `rows` cache rows x n new
@@ -203,9 +210,60 @@ __global__ void __launch_bounds__(256) quantize_append_kernel(const void* __rest
       p = pos_of[r / rows_per_pos];
       fits = p >= 0 && p <= cap - n;
     }
-    quantize_row<F16, QMAX, D>(v ? Xv : Xk, v ? Qv : Qk, v ? Sv : Sk, row, r * cap + (fits ? p : 0) + (row - r * n),
-                               in && fits, i);
+    const int64_t dst = r * cap + (fits ? p : 0) + (row - r * n);
+    quantize_row<F16, QMAX, D>(v ? Xv : Xk, row, code_row<QMAX, D>(v ? Qv : Qk, dst), (v ? Sv : Sk) + dst, in && fits,
+                               i);
   }
+}
+
+// Paged form for serving caches: token t's K and V rows ([tokens, heads, D]
+// each, contiguous) go to cache slot slots[t] = page * page_size + offset of
+// paged caches addressed by strides (codes in bytes, scales in elements), so
+// token-major (NHD) and head-major (HND) pages take the same kernel. A slot
+// outside [0, nslots) (a padding token, marked -1) writes nothing.
+struct PagedDst {
+  uint8_t* q[2];      // K, V codes
+  _Float16* s[2];     // K, V scales
+  int64_t q_page, q_tok, q_head;  // bytes
+  int64_t s_page, s_tok, s_head;  // elements
+  int64_t nslots;
+  int page_log2;
+};
+
+template <bool F16, int QMAX, int D>
+__global__ void __launch_bounds__(256) quantize_pages_kernel(const void* __restrict__ Xk, const void* __restrict__ Xv,
+                                                             const int32_t* __restrict__ slots, int64_t rows,
+                                                             int64_t heads, PagedDst d) {
+  const int i = threadIdx.x & 15;
+  const int64_t rows_per_step = (int64_t)gridDim.x * (blockDim.x >> 4);
+  for (int64_t j = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
+       j - (threadIdx.x >> 4) < 2 * rows; j += rows_per_step) {
+    const bool in = j < 2 * rows;  // the same for the 16 lanes of a row
+    const int v = j >= rows ? 1 : 0;
+    const int64_t row = v ? j - rows : j;  // token row * heads + head
+    const int64_t t = row / heads;
+    const int64_t h = row - t * heads;
+    const int64_t slot = in ? (int64_t)slots[t] : -1;
+    const bool live = slot >= 0 && slot < d.nslots;
+    const int64_t pg = live ? slot >> d.page_log2 : 0;
+    const int64_t off = live ? slot - (pg << d.page_log2) : 0;
+    quantize_row<F16, QMAX, D>(v ? Xv : Xk, row, d.q[v] + pg * d.q_page + off * d.q_tok + h * d.q_head,
+                               d.s[v] + pg * d.s_page + off * d.s_tok + h * d.s_head, live, i);
+  }
+}
+
+template <bool F16, int QMAX>
+hipError_t launch_qp(int D, const void* Xk, const void* Xv, const int32_t* slots, int64_t rows, int64_t heads,
+                     const PagedDst& d, hipStream_t st) {
+  const int64_t want = (2 * rows + 15) / 16;
+  const unsigned grid = (unsigned)(want < (1 << 16) ? want : (1 << 16));
+  if (D == 128)
+    hipLaunchKernelGGL((quantize_pages_kernel<F16, QMAX, 128>), dim3(grid), dim3(256), 0, st, Xk, Xv, slots, rows,
+                       heads, d);
+  else
+    hipLaunchKernelGGL((quantize_pages_kernel<F16, QMAX, 64>), dim3(grid), dim3(256), 0, st, Xk, Xv, slots, rows,
+                       heads, d);
+  return hipGetLastError();
 }
 
 template <bool F16, int QMAX>
@@ -253,6 +311,35 @@ hipError_t launch_quantize_append(int src_f16, int fmt, int D, const void* Xk, c
   if (fmt == KV_I4)
     return src_f16 ? launch_qa<true, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st)
                    : launch_qa<false, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_quantize_pages(int src_f16, int fmt, int D, const void* Xk, const void* Xv, const int32_t* slots,
+                                 int64_t tokens, int64_t heads, void* Qk, void* Qv, void* Sk, void* Sv,
+                                 int64_t num_pages, int page_log2, int64_t q_page, int64_t q_tok, int64_t q_head,
+                                 int64_t s_page, int64_t s_tok, int64_t s_head, hipStream_t st) {
+  if (tokens < 1 || heads < 1 || num_pages < 1 || page_log2 < 0 || page_log2 > 30 || (D != 64 && D != 128))
+    return hipErrorInvalidValue;
+  PagedDst d;
+  d.q[0] = (uint8_t*)Qk;
+  d.q[1] = (uint8_t*)Qv;
+  d.s[0] = (_Float16*)Sk;
+  d.s[1] = (_Float16*)Sv;
+  d.q_page = q_page;
+  d.q_tok = q_tok;
+  d.q_head = q_head;
+  d.s_page = s_page;
+  d.s_tok = s_tok;
+  d.s_head = s_head;
+  d.nslots = num_pages << page_log2;
+  d.page_log2 = page_log2;
+  const int64_t rows = tokens * heads;
+  if (fmt == KV_I8)
+    return src_f16 ? launch_qp<true, 127>(D, Xk, Xv, slots, rows, heads, d, st)
+                   : launch_qp<false, 127>(D, Xk, Xv, slots, rows, heads, d, st);
+  if (fmt == KV_I4)
+    return src_f16 ? launch_qp<true, 7>(D, Xk, Xv, slots, rows, heads, d, st)
+                   : launch_qp<false, 7>(D, Xk, Xv, slots, rows, heads, d, st);
   return hipErrorInvalidValue;
 }
 

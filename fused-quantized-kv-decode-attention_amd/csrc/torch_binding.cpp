@@ -597,6 +597,45 @@ static void quantize_kv_append_at(torch::Tensor Kn, torch::Tensor Vn, torch::Ten
            "launch");
 }
 
+// quantize_kv_to_pages_(K_new[T,Hkv,D], V_new, slot_mapping[T] int32, K_pages[P,page,Hkv,D or D/2], V_pages,
+// Ks_pages[P,page,Hkv], Vs_pages) -> None: token t's K and V rows, quantized as quantize_int8/int4_per_token,
+// into slot slot_mapping[t] = page * page_size + offset of the pages decode_attn_gqa_paged reads (any strided
+// views with a contiguous last dim, so HND storage passes as .permute(0,2,1,3)); slots outside the pages
+// (e.g. -1) are skipped.
+static void quantize_kv_to_pages(torch::Tensor Kn, torch::Tensor Vn, torch::Tensor slots, torch::Tensor Kp,
+                                 torch::Tensor Vp, torch::Tensor Ksp, torch::Tensor Vsp) {
+  check_gpu({&Kn, &Vn, &slots});
+  check_gpu_strided({&Kp, &Vp, &Ksp, &Vsp}, Kn);
+  TORCH_CHECK(Kn.scalar_type() == torch::kHalf || Kn.scalar_type() == torch::kFloat,
+              "fp16: K_new must be float16 or float32");
+  TORCH_CHECK(Kn.dim() == 3 && Vn.sizes() == Kn.sizes() && Vn.scalar_type() == Kn.scalar_type(),
+              "shape: K_new and V_new must be [T,Hkv,D] of one dtype; got ", Kn.sizes(), " and ", Vn.sizes());
+  TORCH_CHECK(Kp.scalar_type() == torch::kChar || Kp.scalar_type() == torch::kByte,
+              "int8: pages must be int8 or packed uint8 (int4)");
+  const int fmt = Kp.scalar_type() == torch::kChar ? FQKV_KV_I8 : FQKV_KV_I4;
+  const int64_t T = Kn.size(0), H = Kn.size(1), D = Kn.size(2);
+  check_D(D);
+  TORCH_CHECK(Kp.dim() == 4 && Kp.size(2) == H && Kp.size(3) == (fmt == FQKV_KV_I8 ? D : D / 2) &&
+                  Vp.sizes() == Kp.sizes() && Vp.strides() == Kp.strides() && Vp.scalar_type() == Kp.scalar_type(),
+              "shape: pages must be [P,page_size,", H, ",", fmt == FQKV_KV_I8 ? "D" : "D/2",
+              "] with equal strides; got ", Kp.sizes(), " and ", Vp.sizes());
+  TORCH_CHECK(Kp.stride(3) == 1, "contig: the last dim of the pages must be contiguous");
+  check_half(Ksp, "Ks_pages");
+  check_half(Vsp, "Vs_pages");
+  TORCH_CHECK(Ksp.sizes() == Kp.sizes().slice(0, 3) && Vsp.sizes() == Ksp.sizes() && Vsp.strides() == Ksp.strides(),
+              "shape: scale pages must be [P,page_size,Hkv] = ", Kp.sizes().slice(0, 3), " with equal strides; got ",
+              Ksp.sizes(), " and ", Vsp.sizes());
+  TORCH_CHECK(slots.scalar_type() == torch::kInt && slots.dim() == 1 && slots.size(0) == T,
+              "shape: slot_mapping must be int32 [T] = [", T, "]");
+  const c10::DeviceGuard guard(Kn.device());
+  check_rc(fqkv_quantize_kv_paged(Kn.data_ptr(), Vn.data_ptr(),
+                                  Kn.scalar_type() == torch::kHalf ? FQKV_SRC_F16 : FQKV_SRC_F32,
+                                  slots.data_ptr<int32_t>(), T, H, D, Kp.data_ptr(), Vp.data_ptr(), Ksp.data_ptr(),
+                                  Vsp.data_ptr(), Kp.size(0), Kp.size(1), Kp.stride(0), Kp.stride(1), Kp.stride(2),
+                                  Ksp.stride(0), Ksp.stride(1), Ksp.stride(2), fmt, cur_stream(Kn)),
+           "launch");
+}
+
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.doc() = "MI355X fused single-query decode attention (fp16 / int8-KV / int4-KV / GQA / GQA split-K)";
   m.def("decode_attn_fp16_mw", &decode_attn_fp16_mw, "fp16 fused decode", py::arg("q"), py::arg("K"), py::arg("V"),
@@ -652,6 +691,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "quantize_kv_append_ with each sequence's position read on the device from pos [B] int32 (graph-capturable)",
         py::arg("K_new"), py::arg("V_new"), py::arg("K_cache"), py::arg("V_cache"), py::arg("Ks_cache"),
         py::arg("Vs_cache"), py::arg("pos"));
+  m.def("quantize_kv_to_pages_", &quantize_kv_to_pages,
+        "quantize new K and V tokens into paged int8 / int4 caches at their slots (in place)", py::arg("K_new"),
+        py::arg("V_new"), py::arg("slot_mapping"), py::arg("K_pages"), py::arg("V_pages"), py::arg("Ks_pages"),
+        py::arg("Vs_pages"));
   m.def("_choose_splits", &choose_splits, "split count the single-block entry points use");
   m.def("_cu_count", &cu_count, "compute units of the current device");
   m.def("_version", []() { return std::string(fqkv_version()); });

@@ -24,6 +24,10 @@ Beyond the reference (same conventions, no counterpart there):
     quantize_kv_append_at_(K_new, V_new, K_cache, V_cache, Ks_cache, Vs_cache, pos[B] int32)
                                                     the same with each sequence's position read
                                                     on the device (graph-capturable)
+    quantize_kv_to_pages_(K_new[T,Hkv,D], V_new, slot_mapping[T] int32, K_pages[P,page,Hkv,·],
+        V_pages, Ks_pages[P,page,Hkv], Vs_pages) -> None
+                                                    the quantizers writing into paged int8 / int4
+                                                    caches at slot = page * page_size + offset
     decode_attn_gqa_nhd(q[B,Hq,D], K[B,N,Hkv,D], V, W, Ks=None, Vs=None) -> o[B,Hq,D]
                                                     token-major (FlashInfer NHD) KV layout
     decode_attn_gqa_strided(q[B,Hq,D], K[B,Hkv,N,D] view, V, W, Ks=None, Vs=None) -> o[B,Hq,D]
@@ -63,6 +67,7 @@ __all__ = [
     "quantize_int4_per_token",
     "quantize_kv_append_",
     "quantize_kv_append_at_",
+    "quantize_kv_to_pages_",
     "decode_attn_gqa_nhd",
     "decode_attn_gqa_strided",
     "decode_attn_gqa_paged",
@@ -74,7 +79,7 @@ __all__ = [
 _ENTRY_POINTS = ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa",
                  "gqa_sk_fast", "decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8",
                  "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token", "quantize_kv_append_",
-                 "quantize_kv_append_at_", "decode_attn_gqa_nhd", "decode_attn_gqa_strided", "decode_attn_gqa_paged")
+                 "quantize_kv_append_at_", "quantize_kv_to_pages_", "decode_attn_gqa_nhd", "decode_attn_gqa_strided", "decode_attn_gqa_paged")
 _EXT = None
 
 

@@ -300,6 +300,27 @@ int fqkv_quantize_kv_append_at(const void* K_new, const void* V_new, int x_dtype
                                const int32_t* pos, int64_t rows_per_pos, int64_t D, int kv_format, void* stream);
 
 /*
+ * The quantizer writing into a paged int8 / int4 cache, as serving engines
+ * fill one: token t of K_new, V_new [tokens, kv_heads, D] (fp16 or fp32,
+ * contiguous) goes to slot slot_mapping[t] = page * page_size + offset (int32,
+ * device memory) of the pages the paged decode entry point reads. Codes of
+ * KV head h of a slot sit at page * page_stride + offset * token_stride +
+ * h * head_stride bytes from K_pages / V_pages (multiples of 8 / 4 / 4 / 2
+ * bytes for int8 D 128 / int8 D 64 / int4 D 128 / int4 D 64), its scale at
+ * the same position in elements by the s_* strides, so token-major (NHD) and
+ * head-major (HND) pages are both served. A slot outside
+ * [0, num_pages * page_size), e.g. -1 for a padding token, writes nothing.
+ * Bytes equal fqkv_quantize_kv's on the same rows. No counterpart in the
+ * reference (its caches are contiguous fp16 / int8 / int4 tensors quantized
+ * on the host); for serving callers of fqkv_decode_attn_gqa_paged.
+ */
+int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, const int32_t* slot_mapping,
+                           int64_t tokens, int64_t kv_heads, int64_t D, void* K_pages, void* V_pages,
+                           void* Ks_pages, void* Vs_pages, int64_t num_pages, int64_t page_size,
+                           int64_t page_stride, int64_t token_stride, int64_t head_stride, int64_t s_page_stride,
+                           int64_t s_token_stride, int64_t s_head_stride, int kv_format, void* stream);
+
+/*
  * Split merge mode for calls that split the sequence (gqa_sk_fast with S > 1
  * and the internal splits of the single-block entry points). Default (0):
  * one kernel per call; the last workgroup of each head group to finish merges

@@ -155,6 +155,28 @@ def test_capi_quantize_append_rejects_bad_args(lib):
     assert f(16, 16, 1, 20, 16, 16, 16, 8, 1, 100, 0, 128, 1, None) == 1 and "aligned" in _err(lib)
 
 
+def test_capi_quantize_paged_rejects_bad_args(lib):
+    """The paged quantizer: slots are read on the GPU (out-of-range ones are skipped there); the
+    host checks format, sizes, the page size, stride and pointer alignment."""
+    f = lib.fqkv_quantize_kv_paged
+    f.argtypes = [VP, VP, ctypes.c_int, VP, I64, I64, I64] + [VP] * 4 + [I64] * 8 + [ctypes.c_int, VP]
+    x = [16, 16, 1, 16]               # K_new, V_new, x_dtype fp32, slot_mapping
+    pages = [16, 16, 16, 16]          # K, V, Ks, Vs pages
+    st = [4096, 256, 128, 32, 2, 1]   # page / token / head strides (bytes), scale strides (elements)
+    assert f(*x, 0, 2, 128, *pages, 8, 16, *st, 1, None) == 0   # zero tokens: nothing to do
+    assert f(*x, 10, 2, 128, *pages, 8, 12, *st, 1, None) == 1 and _err(lib).startswith("page:")
+    assert f(*x, 10, 2, 128, *pages, 0, 16, *st, 1, None) == 1 and _err(lib).startswith("page:")
+    assert f(*x, 10, 0, 128, *pages, 8, 16, *st, 1, None) == 1 and _err(lib).startswith("shape:")
+    assert f(*x, -1, 2, 128, *pages, 8, 16, *st, 1, None) == 1 and _err(lib).startswith("shape:")
+    assert f(*x, 10, 2, 128, *pages, 8, 16, 4096, 252, 128, 32, 2, 1, 1, None) == 1 and _err(lib).startswith("stride:")
+    assert f(*x, 10, 2, 128, *pages, 8, 16, 4096, 256, 128, -32, 2, 1, 1, None) == 1 and _err(lib).startswith("stride:")
+    assert f(*x, 10, 2, 96, *pages, 8, 16, *st, 1, None) == 1 and _err(lib).startswith("D:")
+    assert f(*x, 10, 2, 128, *pages, 8, 16, *st, 0, None) == 1 and "kv_format" in _err(lib)
+    assert f(16, 16, 1, None, 10, 2, 128, *pages, 8, 16, *st, 1, None) == 1 and "null" in _err(lib)
+    assert f(16, 16, 1, 18, 10, 2, 128, *pages, 8, 16, *st, 1, None) == 1 and "slot_mapping" in _err(lib)
+    assert f(*x, 10, 2, 128, 20, 16, 16, 16, 8, 16, *st, 1, None) == 1 and "pages must be" in _err(lib)
+
+
 def test_capi_quantize_append_at_rejects_bad_args(lib):
     """The device-position append: positions are read on the GPU, so the host checks the rest
     (n_new fits the capacity, rows_per_pos divides rows, pointers and their alignment)."""

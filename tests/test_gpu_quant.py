@@ -18,6 +18,10 @@ pytestmark = pytest.mark.gpu
 TOL = 2e-3
 
 
+def draw(g, *shape):
+    return torch.randn(*shape, generator=g, dtype=torch.float32)
+
+
 def edge_rows(D, dtype):
     rows = []
     r = np.zeros(D, np.float32)
@@ -188,6 +192,96 @@ def test_gpu_quantize_append_at_device_positions(dtype, D, fmt):
         fq.quantize_kv_append_at_(Kn, Vn, *got, pos[:4])
     with pytest.raises(RuntimeError, match="^shape: pos"):
         fq.quantize_kv_append_at_(Kn, Vn, *got, pos.long())
+
+
+def page_views(P, page, H, width, qdt, layout):
+    """Sentinel-filled pages [P, page, H, width] and scale pages [P, page, H] as the decode entry point
+    takes them: NHD storage as is, HND storage ([P, H, page, .]) through a permuted view."""
+    def codes(fill):
+        if layout == "nhd":
+            return torch.full((P, page, H, width), fill, dtype=qdt, device="cuda")
+        return torch.full((P, H, page, width), fill, dtype=qdt, device="cuda").permute(0, 2, 1, 3)
+
+    def scales(fill):
+        if layout == "nhd":
+            return torch.full((P, page, H), fill, dtype=torch.float16, device="cuda")
+        return torch.full((P, H, page), fill, dtype=torch.float16, device="cuda").permute(0, 2, 1)
+
+    return codes(0x55), codes(0x33), scales(7.0), scales(9.0)
+
+
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_gpu_quantize_to_pages(fmt, D, dtype, layout):
+    """quantize_kv_to_pages_ writes token t's K and V codes and scales (the quantizer's bytes) at
+    slot_mapping[t] of token-major or head-major pages and nothing else; slots -1 and past the last
+    page are skipped."""
+    P, page, H, T = 6, 16, 2, 40
+    g = torch.Generator().manual_seed(65)
+    width, qdt = (D, torch.int8) if fmt == "int8" else (D // 2, torch.uint8)
+    Kn = (torch.randn(T, H, D, generator=g) * 3).to(dtype).cuda()
+    Vn = (torch.randn(T, H, D, generator=g) * 3).to(dtype).cuda()
+    slots = torch.randperm(P * page, generator=g)[:T].to(torch.int32)
+    slots[3], slots[11], slots[20] = -1, -7, P * page  # padding tokens and a slot past the pages
+    slots[29] = 2 ** 31 - 1
+    pages = page_views(P, page, H, width, qdt, layout)
+    want = [t.clone() for t in pages]
+    fq.quantize_kv_to_pages_(Kn, Vn, slots.cuda(), *pages)
+    qfn = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+    (kq, ks), (vq, vs) = qfn(Kn), qfn(Vn)
+    ok = (slots >= 0) & (slots < P * page)
+    pg, off = (slots[ok] // page).long().cuda(), (slots[ok] % page).long().cuda()
+    sel = ok.nonzero().flatten().cuda()
+    for w, x in zip(want, (kq, vq, ks, vs)):
+        w[pg, off] = x[sel]
+    for got, w in zip(pages, want):
+        assert torch.equal(got, w)
+    with pytest.raises(RuntimeError, match="^shape: slot_mapping"):
+        fq.quantize_kv_to_pages_(Kn, Vn, slots.cuda().long(), *pages)
+    with pytest.raises(RuntimeError, match="^shape: pages"):
+        fq.quantize_kv_to_pages_(Kn[:, :1].contiguous(), Vn[:, :1].contiguous(), slots.cuda(), *pages)
+
+
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_gpu_pages_filled_by_the_quantizer_decode_like_the_oracle(fmt):
+    """A serving-style round trip: three ragged sequences (37, 16, 50 tokens) written into shuffled
+    head-major pages of 16 tokens through their slot mapping, then decode_attn_gqa_paged over
+    those pages against the float64 oracle on the dequantized tokens of each sequence."""
+    B, Hq, Hkv, D, page = 3, 8, 2, 128, 16
+    lens = [37, 16, 50]
+    g = torch.Generator().manual_seed(66)
+    npg = [-(-n // page) for n in lens]
+    P = sum(npg) + 2
+    perm = torch.randperm(P, generator=g).tolist()
+    table = torch.zeros(B, max(npg), dtype=torch.int32)
+    slot_list, K_list, V_list = [], [], []
+    used = 0
+    for b, n in enumerate(lens):
+        ids = perm[used:used + npg[b]]
+        used += npg[b]
+        table[b, :npg[b]] = torch.tensor(ids, dtype=torch.int32)
+        slot_list += [ids[t // page] * page + t % page for t in range(n)]
+        K_list.append(draw(g, n, Hkv, D))
+        V_list.append(draw(g, n, Hkv, D))
+    Kn, Vn = torch.cat(K_list).half().cuda(), torch.cat(V_list).half().cuda()
+    width, qdt = (D, torch.int8) if fmt == "int8" else (D // 2, torch.uint8)
+    Kp, Vp, Ks, Vs = page_views(P, page, Hkv, width, qdt, "hnd")
+    fq.quantize_kv_to_pages_(Kn, Vn, torch.tensor(slot_list, dtype=torch.int32).cuda(), Kp, Vp, Ks, Vs)
+    q = draw(g, B, Hq, D).half()
+    out = fq.decode_attn_gqa_paged(q.cuda(), Kp, Vp, table.cuda(), torch.tensor(lens, dtype=torch.int32).cuda(),
+                                   max(lens), 8, Ks, Vs)
+    deq = quant.dequant_int8 if fmt == "int8" else quant.dequant_int4
+    qfn = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+    start = 0
+    for b, n in enumerate(lens):
+        (kq, ks), (vq, vs) = qfn(Kn[start:start + n]), qfn(Vn[start:start + n])
+        Kf = deq(kq, ks).permute(1, 0, 2).cpu().double().numpy()  # [Hkv, n, D]
+        Vf = deq(vq, vs).permute(1, 0, 2).cpu().double().numpy()
+        ref = oracle.gqa_attention(q[b:b + 1].numpy(), Kf[None], Vf[None])[0]
+        assert float(np.abs(out[b].float().cpu().numpy().astype(np.float64) - ref).max()) <= TOL
+        start += n
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
