@@ -157,7 +157,11 @@ int check_common(int64_t N, int64_t D, int64_t W) {
 
 // Single-block style decode: rows KV rows, G query heads per row. Splits the
 // sequence internally when rows alone cannot fill the GPU and the workspace allows.
-int64_t row_bytes_of(int fmt, int64_t D) { return fmt == KV_F16 ? 2 * D : (fmt == KV_I8 ? D : D / 2); }
+int64_t row_bytes_of(int fmt, int64_t D) {
+  return (fmt == KV_F16 || fmt == KV_BF16) ? 2 * D : (fmt == KV_I8 ? D : D / 2);
+}
+// int8 / int4: codes with per-token scales
+bool is_quant(int fmt) { return fmt == KV_I8 || fmt == KV_I4; }
 
 // KV layout of a single-block call (null: the reference's contiguous layout).
 struct Layout {
@@ -286,7 +290,7 @@ int sk_fast(int fmt, const void* q, const void* K, const void* V, const void* Ks
   if (S < 1 || S > (1 << 20)) return fail(FQKV_ERR_ARG, "S: split count must be in [1, 2^20], got %lld", (long long)S);
   if (Hq < 1 || Hkv < 1 || Hq % Hkv != 0)
     return fail(FQKV_ERR_ARG, "heads: Hq (%lld) must be a positive multiple of Hkv (%lld)", (long long)Hq, (long long)Hkv);
-  if (fmt == KV_F16) {
+  if (!is_quant(fmt)) {
     rc = check_ptrs_kv(q, K, V, o);
   } else {
     rc = check_ptrs_quant(fmt, D, q, K, V, Ks, Vs, o);
@@ -534,9 +538,9 @@ int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const vo
 static int check_layout_common(int fmt, int64_t D, const void* q, const void* K, const void* V,
                                const void* Ks, const void* Vs, const void* o, int64_t kv_bs, int64_t kv_hs,
                                int64_t kv_ts, int64_t sc_bs, int64_t sc_hs, int64_t sc_ts) {
-  if (fmt != FQKV_KV_F16 && fmt != FQKV_KV_I8 && fmt != FQKV_KV_I4)
-    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_F16, FQKV_KV_I8 or FQKV_KV_I4");
-  int rc = fmt == KV_F16 ? check_ptrs_kv(q, K, V, o) : check_ptrs_quant(fmt, D, q, K, V, Ks, Vs, o);
+  if (fmt != FQKV_KV_F16 && fmt != FQKV_KV_I8 && fmt != FQKV_KV_I4 && fmt != FQKV_KV_BF16)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_F16, FQKV_KV_BF16, FQKV_KV_I8 or FQKV_KV_I4");
+  int rc = !is_quant(fmt) ? check_ptrs_kv(q, K, V, o) : check_ptrs_quant(fmt, D, q, K, V, Ks, Vs, o);
   if (rc) return rc;
   const int64_t rb = row_bytes_of(fmt, D);
   const int64_t al = (fmt == KV_I4 && D == 64) ? 8 : 16;
@@ -544,7 +548,7 @@ static int check_layout_common(int fmt, int64_t D, const void* q, const void* K,
     return fail(FQKV_ERR_ARG, "strides: KV token stride must be >= %lld bytes and all KV strides multiples of %lld "
                 "bytes, got batch %lld, head %lld, token %lld", (long long)rb, (long long)al, (long long)kv_bs,
                 (long long)kv_hs, (long long)kv_ts);
-  if (fmt != KV_F16 && (sc_ts < 1 || sc_ts > INT_MAX / 2 || sc_hs < 0 || sc_bs < 0))
+  if (is_quant(fmt) && (sc_ts < 1 || sc_ts > INT_MAX / 2 || sc_hs < 0 || sc_bs < 0))
     return fail(FQKV_ERR_ARG, "strides: scale strides must be non-negative with a token stride >= 1");
   return FQKV_OK;
 }
@@ -563,7 +567,7 @@ int fqkv_decode_attn_gqa_strided(const void* q, const void* K, const void* V, co
                                 kv_token_stride, sc_batch_stride, sc_head_stride, sc_token_stride)))
     return rc;
   if ((N + SPAN_MARGIN_TOKENS) * kv_token_stride > ROW_SPAN ||
-      (kv_format != KV_F16 && 2 * (N + SPAN_MARGIN_TOKENS) * sc_token_stride > ROW_SPAN))
+      (is_quant(kv_format) && 2 * (N + SPAN_MARGIN_TOKENS) * sc_token_stride > ROW_SPAN))
     return fail(FQKV_ERR_ARG, "N: %lld tokens at a %lld-byte stride exceed the per-row span (4 GiB less %lld tokens)",
                 (long long)N, (long long)kv_token_stride, (long long)SPAN_MARGIN_TOKENS);
   Layout L{Hkv, kv_batch_stride, kv_head_stride, kv_token_stride, sc_batch_stride, sc_head_stride, sc_token_stride,

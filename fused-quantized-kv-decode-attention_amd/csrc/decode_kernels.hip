@@ -642,6 +642,19 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
     for (int i = 0; i < F::NKI; ++i) qb[i] = F::qfrag(rQ, qrow * D, i, R);
   }
+  // bf16 products take the fp16 query as two bf16 operands, q = hi + lo
+  // exactly (hi holds 8 of q's 11 significant bits, lo the rest)
+  bf8_t qhi[F::BF16 ? F::NKI : 1], qlo[F::BF16 ? F::NKI : 1];
+  if constexpr (F::BF16) {
+#pragma unroll
+    for (int i = 0; i < F::NKI; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = (float)qb[i][e];
+        qhi[i][e] = (__bf16)f;
+        qlo[i][e] = (__bf16)(f - (float)qhi[i][e]);
+      }
+  }
   // int8 / int4 scores come out of the matrix cores as 2^-24 (q.k + BIAS
   // sum(q)) over the query as the operands carry it; qbias = BIAS sum(q) of
   // the lane's column (zero for fp16)
@@ -845,8 +858,15 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       if constexpr (F::STAGE_K) F::stage_k(s_kstage + w * F::KSTAGE, lane, kr[u]);
       c4[u] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int i = 0; i < F::NKI; ++i)
-        c4[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(F::kfrag(kr[u], i), qb[i], c4[u], 0, 0, 0);
+      for (int i = 0; i < F::NKI; ++i) {
+        if constexpr (F::BF16) {
+          const bf8_t kf = __builtin_bit_cast(bf8_t, F::kfrag(kr[u], i));
+          c4[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qhi[i], c4[u], 0, 0, 0);
+          c4[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qlo[i], c4[u], 0, 0, 0);
+        } else {
+          c4[u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(F::kfrag(kr[u], i), qb[i], c4[u], 0, 0, 0);
+        }
+      }
     }
 
     // scores of the lane's tiles; tokens past the split (or on a bad page)
@@ -926,18 +946,33 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
           for (int k = 0; k < 4; ++k) s_pw[((g * P + jl) * 16 + 4 * R + k) * HG + hh] = wv[k];
         }
       }
-      // hi through an explicit conversion (round toward zero): converting
-      // with a cast lets the compiler fuse the product into a mixed-precision
-      // multiply-add for one use and not another, and the two roundings of w
-      // to fp16 can differ, leaving hi + lo an fp16 ulp off w
-      const h2_t h01 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(wv[0], wv[1]));
-      const h2_t h23 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(wv[2], wv[3]));
-      const h2_t l01 = __builtin_bit_cast(
-          h2_t, __builtin_amdgcn_cvt_pkrtz(wv[0] - (float)h01.x, wv[1] - (float)h01.y));
-      const h2_t l23 = __builtin_bit_cast(
-          h2_t, __builtin_amdgcn_cvt_pkrtz(wv[2] - (float)h23.x, wv[3] - (float)h23.y));
-      phi[g] = h4_t{h01.x, h01.y, h23.x, h23.y};
-      plo[g] = h4_t{l01.x, l01.y, l23.x, l23.y};
+      if constexpr (F::BF16) {
+        // bf16 pairs by truncation: hi = the top 16 bits of w (exact as an
+        // fp32 value), lo = the top 16 bits of w - hi; |w - hi - lo| < 2^-16 |w|
+        uint32_t bh4[4], bl4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          bh4[k] = __builtin_bit_cast(uint32_t, wv[k]) & 0xFFFF0000u;
+          bl4[k] = __builtin_bit_cast(uint32_t, wv[k] - __builtin_bit_cast(float, bh4[k]));
+        }
+        // the high halves of two dwords -> one dword of two bf16 (element 0 low)
+        auto hi2 = [](uint32_t a, uint32_t b) { return __builtin_amdgcn_perm(b, a, 0x07060302u); };
+        phi[g] = __builtin_bit_cast(h4_t, u2_t{hi2(bh4[0], bh4[1]), hi2(bh4[2], bh4[3])});
+        plo[g] = __builtin_bit_cast(h4_t, u2_t{hi2(bl4[0], bl4[1]), hi2(bl4[2], bl4[3])});
+      } else {
+        // hi through an explicit conversion (round toward zero): converting
+        // with a cast lets the compiler fuse the product into a mixed-precision
+        // multiply-add for one use and not another, and the two roundings of w
+        // to fp16 can differ, leaving hi + lo an fp16 ulp off w
+        const h2_t h01 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(wv[0], wv[1]));
+        const h2_t h23 = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(wv[2], wv[3]));
+        const h2_t l01 = __builtin_bit_cast(
+            h2_t, __builtin_amdgcn_cvt_pkrtz(wv[0] - (float)h01.x, wv[1] - (float)h01.y));
+        const h2_t l23 = __builtin_bit_cast(
+            h2_t, __builtin_amdgcn_cvt_pkrtz(wv[2] - (float)h23.x, wv[3] - (float)h23.y));
+        phi[g] = h4_t{h01.x, h01.y, h23.x, h23.y};
+        plo[g] = h4_t{l01.x, l01.y, l23.x, l23.y};
+      }
     }
     const float acc_alpha = F::QUANT ? __builtin_amdgcn_ldexpf(alpha, shift - acc_shift) : alpha;
     l_run = l_run * acc_alpha + psum;
@@ -1031,10 +1066,20 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
       for (int c = 0; c < VE; ++c) {
         vf[c] = __builtin_shufflevector(vfrag<FMT, D>(vr[u], c), vfrag<FMT, D>(vr[u + 1], c), 0, 1, 2, 3, 4, 5, 6, 7);
-        acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[c], bh, acc[c], 0, 0, 0);
+        if constexpr (F::BF16)
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8_t, vf[c]),
+                                                           __builtin_bit_cast(bf8_t, bh), acc[c], 0, 0, 0);
+        else
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[c], bh, acc[c], 0, 0, 0);
       }
 #pragma unroll
-      for (int c = 0; c < VE; ++c) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[c], bl, acc[c], 0, 0, 0);
+      for (int c = 0; c < VE; ++c) {
+        if constexpr (F::BF16)
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8_t, vf[c]),
+                                                           __builtin_bit_cast(bf8_t, bl), acc[c], 0, 0, 0);
+        else
+          acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[c], bl, acc[c], 0, 0, 0);
+      }
     }
   }
 
@@ -1278,6 +1323,8 @@ hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, i
                                : launch_partial_d<KV_I8, 128>(hg, p, nblocks, nw, st);
     case KV_I4: return D == 64 ? launch_partial_d<KV_I4, 64>(hg, p, nblocks, nw, st)
                                : launch_partial_d<KV_I4, 128>(hg, p, nblocks, nw, st);
+    case KV_BF16: return D == 64 ? launch_partial_d<KV_BF16, 64>(hg, p, nblocks, nw, st)
+                                 : launch_partial_d<KV_BF16, 128>(hg, p, nblocks, nw, st);
   }
   return hipErrorInvalidValue;
 }

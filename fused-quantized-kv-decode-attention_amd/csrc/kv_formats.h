@@ -43,13 +43,14 @@
 namespace fqkv {
 
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
 
-enum KvFormat : int { KV_F16 = 0, KV_I8 = 1, KV_I4 = 2 };
+enum KvFormat : int { KV_F16 = 0, KV_I8 = 1, KV_I4 = 2, KV_BF16 = 3 };
 
 // v_perm_b32 byte selector: 0-3 pick bytes of the second operand, 4-7 of
 // the first, 0x0C gives a zero byte.
@@ -153,6 +154,7 @@ struct Fmt;
 template <int D>
 struct Fmt<KV_F16, D> {
   static constexpr bool QUANT = false;
+  static constexpr bool BF16 = false;  // operands are fp16 bit patterns
   static constexpr bool STAGE_K = true;
   // tile offsets in the loads' SGPR offset (instead of VGPR adds per load):
   // for the VALU-bound int4 only; the scalar work ahead of the first loads
@@ -209,10 +211,21 @@ struct Fmt<KV_F16, D> {
   }
 };
 
+// ---------------------------------------------------------------- bf16 ----
+// bf16 K and V move exactly like fp16 (16-bit elements: the same loads, LDS
+// staging and exchanges, the same bit patterns in the operand registers); only
+// the matrix-core products differ, which take bf16 operands (the query and
+// the weights as bf16 pairs, hi + lo, so neither loses precision).
+template <int D>
+struct Fmt<KV_BF16, D> : Fmt<KV_F16, D> {
+  static constexpr bool BF16 = true;
+};
+
 // ---------------------------------------------------------------- int8 ----
 template <int D>
 struct Fmt<KV_I8, D> {
   static constexpr bool QUANT = true;
+  static constexpr bool BF16 = false;
   static constexpr bool STAGE_K = false;
   static constexpr bool SOFF_TILE = false;
   static constexpr int ROWB = D;
@@ -256,6 +269,7 @@ struct Fmt<KV_I8, D> {
 template <int D>
 struct Fmt<KV_I4, D> {
   static constexpr bool QUANT = true;
+  static constexpr bool BF16 = false;
   static constexpr bool STAGE_K = false;
   static constexpr bool SOFF_TILE = true;
   static constexpr int ROWB = D / 2;

@@ -313,19 +313,22 @@ void gqa_sk_fast_int4(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::
 
 // ---- other KV layouts (no counterpart in the reference) ----
 
+// int8 / int4 codes, which come with per-token scales
+bool quant_fmt(int fmt) { return fmt == FQKV_KV_I8 || fmt == FQKV_KV_I4; }
+
 // KV format from K's dtype; returns FQKV_KV_*, sets D (unpacked head_dim) and the element size.
 int kv_format_of(const torch::Tensor& K, int64_t* D, int64_t* elem) {
-  if (K.scalar_type() == torch::kHalf) {
+  if (K.scalar_type() == torch::kHalf || K.scalar_type() == torch::kBFloat16) {
     *D = K.size(-1);
     *elem = 2;
-    return FQKV_KV_F16;
+    return K.scalar_type() == torch::kHalf ? FQKV_KV_F16 : FQKV_KV_BF16;
   }
   if (K.scalar_type() == torch::kChar) {
     *D = K.size(-1);
     *elem = 1;
     return FQKV_KV_I8;
   }
-  TORCH_CHECK(K.scalar_type() == torch::kByte, "fp16: K must be float16, int8 or packed uint8 (int4)");
+  TORCH_CHECK(K.scalar_type() == torch::kByte, "fp16: K must be float16, bfloat16, int8 or packed uint8 (int4)");
   *D = 2 * K.size(-1);
   *elem = 1;
   return FQKV_KV_I4;
@@ -333,7 +336,7 @@ int kv_format_of(const torch::Tensor& K, int64_t* D, int64_t* elem) {
 
 void check_scales(int fmt, const c10::optional<torch::Tensor>& Ks, const c10::optional<torch::Tensor>& Vs,
                   at::IntArrayRef want) {
-  if (fmt == FQKV_KV_F16) return;
+  if (!quant_fmt(fmt)) return;
   TORCH_CHECK(Ks.has_value() && Vs.has_value(), "int8: int8 / int4 K and V need per-token scales Ks and Vs");
   check_gpu_strided({&*Ks, &*Vs}, *Ks);
   check_half(*Ks, "Ks");
@@ -361,7 +364,8 @@ torch::Tensor decode_attn_gqa_nhd(torch::Tensor q, torch::Tensor K, torch::Tenso
   TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
   TORCH_CHECK(N >= 1, "N: need at least one cached token");
   check_scales(fmt, Ks, Vs, {B, N, Hkv});
-  if (fmt != FQKV_KV_F16) {
+  const bool quant = quant_fmt(fmt);
+  if (quant) {
     TORCH_CHECK(Ks->device() == q.device(), "cuda: all tensors must be on the same device");
     TORCH_CHECK(Ks->is_contiguous() && Vs->is_contiguous(), "contig: scales must be contiguous");
   }
@@ -370,8 +374,8 @@ torch::Tensor decode_attn_gqa_nhd(torch::Tensor q, torch::Tensor K, torch::Tenso
   auto ws = workspace_for(q, B * Hkv, Hq / Hkv, N, D, fmt, W);
   const int64_t rb = K.size(3) * elem;
   check_rc(fqkv_decode_attn_gqa_strided(q.data_ptr(), K.data_ptr(), V.data_ptr(),
-                                        fmt == FQKV_KV_F16 ? nullptr : Ks->data_ptr(),
-                                        fmt == FQKV_KV_F16 ? nullptr : Vs->data_ptr(), o.data_ptr(), B, Hq, Hkv, N, D,
+                                        quant ? Ks->data_ptr() : nullptr, quant ? Vs->data_ptr() : nullptr,
+                                        o.data_ptr(), B, Hq, Hkv, N, D,
                                         fmt, N * Hkv * rb, rb, Hkv * rb, N * Hkv, 1, Hkv, W,
                                         ws.defined() ? ws.data_ptr() : nullptr, ws.defined() ? ws.numel() : 0,
                                         cur_stream(q)),
@@ -402,11 +406,11 @@ torch::Tensor decode_attn_gqa_strided(torch::Tensor q, torch::Tensor K, torch::T
   TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
   TORCH_CHECK(N >= 1, "N: need at least one cached token");
   check_scales(fmt, Ks, Vs, {B, Hkv, N});
-  if (fmt != FQKV_KV_F16) TORCH_CHECK(Ks->device() == q.device(), "cuda: all tensors must be on the same device");
+  const bool quant = quant_fmt(fmt);
+  if (quant) TORCH_CHECK(Ks->device() == q.device(), "cuda: all tensors must be on the same device");
   const c10::DeviceGuard guard(q.device());
   auto o = torch::empty({B, Hq, D}, q.options());
   auto ws = workspace_for(q, B * Hkv, Hq / Hkv, N, D, fmt, W);
-  const bool quant = fmt != FQKV_KV_F16;
   check_rc(fqkv_decode_attn_gqa_strided(q.data_ptr(), K.data_ptr(), V.data_ptr(), quant ? Ks->data_ptr() : nullptr,
                                         quant ? Vs->data_ptr() : nullptr, o.data_ptr(), B, Hq, Hkv, N, D, fmt,
                                         K.stride(0) * elem, K.stride(1) * elem, K.stride(2) * elem,
@@ -446,13 +450,13 @@ torch::Tensor decode_attn_gqa_paged(torch::Tensor q, torch::Tensor Kp, torch::Te
   TORCH_CHECK(Hkv >= 1 && Hq % Hkv == 0, "heads: Hq (", Hq, ") must be a multiple of Hkv (", Hkv, ")");
   TORCH_CHECK(max_seq_len >= 1, "N: max_seq_len must be >= 1");
   check_scales(fmt, Ks, Vs, {P, page, Hkv});
-  if (fmt != FQKV_KV_F16) TORCH_CHECK(Ks->device() == q.device(), "cuda: all tensors must be on the same device");
+  const bool qz = quant_fmt(fmt);
+  if (qz) TORCH_CHECK(Ks->device() == q.device(), "cuda: all tensors must be on the same device");
   const c10::DeviceGuard guard(q.device());
   auto o = torch::empty({B, Hq, D}, q.options());
   const int64_t max_pages = page_table.size(1);
   const int64_t N = std::min<int64_t>(max_seq_len, max_pages * page);
   auto ws = workspace_for(q, B * Hkv, Hq / Hkv, N, D, fmt, W);
-  const bool qz = fmt != FQKV_KV_F16;
   check_rc(fqkv_decode_attn_gqa_paged(q.data_ptr(), Kp.data_ptr(), Vp.data_ptr(), qz ? Ks->data_ptr() : nullptr,
                                       qz ? Vs->data_ptr() : nullptr, page_table.data_ptr<int32_t>(),
                                       seq_lens.data_ptr<int32_t>(), o.data_ptr(), B, Hq, Hkv, P, max_pages, page,

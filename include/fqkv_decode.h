@@ -53,7 +53,11 @@ enum {
   FQKV_ERR_HIP = 2  /* a HIP runtime call or kernel launch failed */
 };
 
-enum { FQKV_KV_F16 = 0, FQKV_KV_I8 = 1, FQKV_KV_I4 = 2 };
+/* KV element formats: fp16 (the reference's), int8 and packed int4 codes with
+ * fp16 per-token scales (the reference's quantized formats), and bf16 (no
+ * counterpart in the reference; accepted by the strided and paged entry
+ * points, for caches kept in a bf16 model's own dtype). */
+enum { FQKV_KV_F16 = 0, FQKV_KV_I8 = 1, FQKV_KV_I4 = 2, FQKV_KV_BF16 = 3 };
 
 enum { FQKV_SRC_F16 = 0, FQKV_SRC_F32 = 1 }; /* element type of a quantizer input */
 
@@ -175,11 +179,11 @@ int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const vo
                            int64_t CW, void* stream);
 
 /*
- * GQA-aware decode over a KV cache in any strided layout (fp16, int8 or int4
- * per kv_format): KV head h of sequence b starts at
+ * GQA-aware decode over a KV cache in any strided layout (fp16, bf16, int8
+ * or int4 per kv_format): KV head h of sequence b starts at
  * K + b*kv_batch_stride + h*kv_head_stride and its tokens lie kv_token_stride
- * bytes apart (each token row is D fp16 / D int8 / D/2 packed bytes); scales
- * likewise in fp16 elements (ignored for fp16). [B, Hkv, N, D] is the
+ * bytes apart (each token row is D fp16 or bf16 / D int8 / D/2 packed bytes);
+ * scales likewise in fp16 elements (ignored for fp16 and bf16). [B, Hkv, N, D] is the
  * reference layout; [B, N, Hkv, D] (FlashInfer's NHD, flashinfer_looptimed.py:63-65)
  * has kv_token_stride = Hkv*row_bytes, kv_head_stride = row_bytes,
  * kv_batch_stride = N*Hkv*row_bytes. q [B, Hq, D], o [B, Hq, D] fp16.
@@ -198,8 +202,8 @@ int fqkv_decode_attn_gqa_strided(const void* q, const void* K, const void* V, co
  * (int32, device) at in-page position t % page_size. Within page pg, KV head h
  * starts at K_pages + pg*kv_page_stride + h*kv_head_stride, tokens
  * kv_token_stride bytes apart (NHD pages [num_pages, page_size, Hkv, D] and
- * HND pages [num_pages, Hkv, page_size, D] are both strides); scales alike in
- * elements. page_size: a power of two >= 16. max_seq_len bounds every
+ * HND pages [num_pages, Hkv, page_size, D] are both strides; any kv_format);
+ * scales alike in elements. page_size: a power of two >= 16. max_seq_len bounds every
  * seq_lens[b] (longer sequences are cut there; the kernel also never reads past
  * max_pages pages); a page id outside [0, num_pages) contributes nothing.
  * No counterpart in the reference.

@@ -1,7 +1,8 @@
 """KV layouts beyond the reference's contiguous [B, Hkv, N, D]: the token-major
 [B, N, Hkv, D] layout FlashInfer uses (flashinfer_looptimed.py:63-65) and paged
 caches (NHD pages, HND pages as a strided view), for fp16, int8 and int4, with
-ragged sequence lengths. Checked against the float64 oracle at max-abs 2e-3;
+ragged sequence lengths; and bf16 caches (no counterpart in the reference) in
+every layout. Checked against the float64 oracle at max-abs 2e-3;
 the token-major layout also bit for bit against the contiguous entry point,
 since only addresses differ."""
 
@@ -89,8 +90,9 @@ def paged_cache(g, lens, Hkv, D, page, fmt, hnd=False, spare=3):
         table[b, :n] = ids[k:k + n].to(torch.int32)
         k += n
     X = draw(g, 2, P, page, Hkv, D)  # raw K and V pages, NHD
-    if fmt == "fp16":
-        Kp, Vp = X[0].half(), X[1].half()
+    if fmt in ("fp16", "bf16"):
+        dt = torch.float16 if fmt == "fp16" else torch.bfloat16
+        Kp, Vp = X[0].to(dt), X[1].to(dt)
         Kf, Vf = Kp.float().numpy(), Vp.float().numpy()
         Ks = Vs = None
     else:
@@ -116,7 +118,7 @@ def paged_cache(g, lens, Hkv, D, page, fmt, hnd=False, spare=3):
     return Kp, Vp, Ks, Vs, table.cuda(), torch.tensor(lens, dtype=torch.int32).cuda(), seqs
 
 
-@pytest.mark.parametrize("fmt", ["fp16", "int8", "int4"])
+@pytest.mark.parametrize("fmt", ["fp16", "bf16", "int8", "int4"])
 @pytest.mark.parametrize("page,hnd", [(16, False), (64, True), (256, False)])
 def test_paged(fmt, page, hnd):
     g = torch.Generator().manual_seed(52)
@@ -217,7 +219,7 @@ def test_strided_rejects_bad_views():
         fq.decode_attn_gqa_strided(q, Kb, Kb, 8)
 
 
-@pytest.mark.parametrize("fmt", ["fp16", "int8", "int4"])
+@pytest.mark.parametrize("fmt", ["fp16", "bf16", "int8", "int4"])
 @pytest.mark.parametrize("lens", [[0, 5, 0, 300], [0, 20000, 0]])
 def test_paged_empty_sequences_give_zeros(fmt, lens):
     """A batch slot with seq_len 0 (continuous batching) has no keys: its output
@@ -234,3 +236,53 @@ def test_paged_empty_sequences_give_zeros(fmt, lens):
         else:
             ref = oracle.gqa_attention(q.numpy()[b:b + 1], Kb[None], Vb[None])[0]
             assert maxerr(out[b], ref) <= TOL, (b, lens[b])
+
+
+# ------------------------------------------------------------------ bf16 ----
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("G", [1, 2, 4, 8, 16])
+@pytest.mark.parametrize("N", [1, 100, 3000, 20000])
+def test_bf16_strided_against_the_oracle(N, G, D):
+    """bf16 K and V through decode_attn_gqa_strided (a view of a larger cache) at every head-group
+    width, from one token to the internally split 20000: the matrix-core products take the query
+    and the weights as bf16 pairs, so the output is as close to the float64 oracle on the bf16
+    values as the fp16 path's is."""
+    g = torch.Generator().manual_seed(57 + N + G + D)
+    B, Hkv = 2, 2
+    Hq = G * Hkv
+    q = draw(g, B, Hq, D).half()
+    Kc, Vc = draw(g, B, Hkv, N + 7, D).bfloat16(), draw(g, B, Hkv, N + 7, D).bfloat16()
+    K, V = Kc[:, :, :N], Vc[:, :, :N]
+    out = fq.decode_attn_gqa_strided(q.cuda(), Kc.cuda()[:, :, :N], Vc.cuda()[:, :, :N], 8)
+    ref = oracle.gqa_attention(q.numpy(), K.float().numpy(), V.float().numpy())
+    assert maxerr(out, ref) <= TOL
+
+
+def test_bf16_nhd_equals_strided_and_the_oracle():
+    g = torch.Generator().manual_seed(58)
+    B, Hq, Hkv, N, D = 2, 32, 8, 1500, 128
+    q = draw(g, B, Hq, D).half()
+    K, V = draw(g, B, N, Hkv, D).bfloat16(), draw(g, B, N, Hkv, D).bfloat16()
+    a = fq.decode_attn_gqa_nhd(q.cuda(), K.cuda(), V.cuda(), 8)
+    b = fq.decode_attn_gqa_strided(q.cuda(), K.cuda().transpose(1, 2), V.cuda().transpose(1, 2), 8)
+    assert torch.equal(a, b)
+    ref = oracle.gqa_attention(q.numpy(), K.float().numpy().transpose(0, 2, 1, 3),
+                               V.float().numpy().transpose(0, 2, 1, 3))
+    assert maxerr(a, ref) <= TOL
+
+
+def test_bf16_keys_beyond_the_fp16_range():
+    """Keys outside fp16's range (elements up to ~1e5, and ~1e-6, below fp16's normal range) are
+    exact in bf16 and must neither overflow nor lose precision in the products: a score of ~2e5
+    picks one token for head 0, the other heads weigh every token almost alike."""
+    g = torch.Generator().manual_seed(59)
+    B, Hq, Hkv, N, D = 1, 4, 1, 64, 64
+    q = draw(g, B, Hq, D).half()
+    K = (draw(g, B, Hkv, N, D) * 1e-6).bfloat16()
+    V = (draw(g, B, Hkv, N, D) * 1e-3).bfloat16()
+    K[0, 0, 9] = (q[0, 0].float() * 3e4).bfloat16()  # elements past fp16's 65504; a dot of ~2e6 for head 0
+    out = fq.decode_attn_gqa_strided(q.cuda(), K.cuda(), V.cuda(), 8)
+    ref = oracle.gqa_attention(q.numpy(), K.float().numpy(), V.float().numpy())
+    assert np.isfinite(out.float().cpu().numpy()).all()
+    assert maxerr(out, ref) <= 1e-5
