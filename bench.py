@@ -621,22 +621,24 @@ def suite_splitk_quant(torch, fq, steps, warmup, rows):
 
 def suite_paged(torch, fq, steps, warmup, rows):
     """decode_attn_gqa_paged (Hq 32, Hkv 8, D 128, B 8, N 32768) over NHD pages of 16 / 64 / 256
-    tokens and head-major (HND) pages of 64 tokens at shuffled page ids, fp16 / int8 / int4, next
-    to the contiguous decode_attn_gqa[_int8|_int4] over the same tokens: what the page indirection
-    costs at a 1 GB cache."""
+    tokens and head-major (HND) pages of 64 tokens at shuffled page ids, fp16 / bf16 / int8 / int4,
+    next to the contiguous decode_attn_gqa[_int8|_int4] (bf16: decode_attn_gqa_strided) over the
+    same tokens: what the page indirection costs at a 1 GB cache."""
     B, Hq, Hkv, N, Dd, W = 8, 32, 8, 32768, 128, 8
     G = Hq // Hkv
     g = torch.Generator(device="cuda").manual_seed(11)
     q = torch.randn(B, Hq, Dd, device="cuda", generator=g).half()
     sl = torch.full((B,), N, dtype=torch.int32, device="cuda")
     nsteps, nwarm = max(50, steps // 4), max(10, warmup // 4)
-    for fmt in ("fp16", "int8", "int4"):
+    for fmt in ("fp16", "bf16", "int8", "int4"):
         Xk = torch.randn(B * Hkv, N, Dd, device="cuda", generator=g)
         Xv = torch.randn(B * Hkv, N, Dd, device="cuda", generator=g)
-        if fmt == "fp16":
-            K, V, Ks, Vs = Xk.half(), Xv.half(), None, None
+        if fmt in ("fp16", "bf16"):
+            dt = torch.float16 if fmt == "fp16" else torch.bfloat16
+            K, V, Ks, Vs = Xk.to(dt), Xv.to(dt), None, None
             Kf, Vf = K[:Hkv].float(), V[:Hkv].float()
-            contiguous = lambda: fq.decode_attn_gqa(q, K.view(B, Hkv, N, Dd), V.view(B, Hkv, N, Dd), W)
+            entry = fq.decode_attn_gqa if fmt == "fp16" else fq.decode_attn_gqa_strided
+            contiguous = lambda: entry(q, K.view(B, Hkv, N, Dd), V.view(B, Hkv, N, Dd), W)
             kvb = 4 * Hkv * N * Dd
         else:
             quantize = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token

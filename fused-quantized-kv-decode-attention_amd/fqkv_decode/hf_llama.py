@@ -11,8 +11,9 @@ Decode calls take the kernel path when the kernel computes exactly what SDPA
 would: query length 1, no attention mask (no padding), no dropout, no
 sliding window or soft-capping, head_dim 64 or 128, Hq a multiple of Hkv and
 the softmax scale 1/sqrt(head_dim). Anything else falls back to SDPA. As in
-the reference, non-fp16 tensors are converted to fp16 for the kernel and the
-output is cast back to the query's dtype.
+the reference, the query goes to the kernel in fp16 and the output is cast
+back to the query's dtype; a bf16 model's KV cache is read in bf16 as it is
+(``decode_attn_gqa_strided``), other dtypes are converted to fp16.
 
 Usage::
 
@@ -91,12 +92,16 @@ def attention_forward(module, query, key, value, attention_mask=None, scaling=No
     if getattr(module, "training", False) or not kernel_applies(query, key, attention_mask, scaling, dropout,
                                                                **kwargs):
         return _sdpa(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
-    from . import decode_attn_gqa
+    from . import decode_attn_gqa, decode_attn_gqa_strided
 
     q = query[:, :, 0, :].to(torch.float16).contiguous()  # [B, Hq, D]
-    K = key.to(torch.float16).contiguous()                 # [B, Hkv, N, D]
-    V = value.to(torch.float16).contiguous()
-    out = decode_attn_gqa(q, K, V, _W)                     # [B, Hq, D]
+    if key.dtype == torch.bfloat16 and key.stride(-1) == 1 and value.stride() == key.stride():
+        # a bf16 model's cache is read as it is (no per-step conversion of the whole cache)
+        out = decode_attn_gqa_strided(q, key, value, _W)
+    else:
+        K = key.to(torch.float16).contiguous()             # [B, Hkv, N, D]
+        V = value.to(torch.float16).contiguous()
+        out = decode_attn_gqa(q, K, V, _W)                 # [B, Hq, D]
     return out.unsqueeze(1).to(query.dtype), None          # [B, 1, Hq, D]
 
 
@@ -112,7 +117,8 @@ def _static_attention(module, query, key, value, attention_mask, scaling, dropou
     # may hide positions below the length: that step goes to SDPA with the mask
     ok = (qlen == 1 and not dropout and not getattr(module, "training", False) and query.is_cuda
           and not getattr(attention_mask, "fqkv_padding", False)
-          and (key.dtype == torch.float16 or ks is not None) and D in (64, 128) and Hq % key.shape[1] == 0
+          and (key.dtype in (torch.float16, torch.bfloat16) or ks is not None) and D in (64, 128)
+          and Hq % key.shape[1] == 0
           and kwargs.get("sliding_window") is None and kwargs.get("softcap") is None
           and (scaling is None or abs(scaling * math.sqrt(D) - 1.0) <= 1e-6))
     if not ok:
@@ -423,7 +429,7 @@ _STATIC_LAYER_CLASSES = None
 
 
 def StaticKVCache(config, max_cache_len, kv_format=None):
-    """A transformers ``Cache`` of preallocated fp16 KV buffers with the sequence lengths on the
+    """A transformers ``Cache`` of preallocated KV buffers (the model's fp16 or bf16) with the sequence lengths on the
     device, for decode steps captured in a HIP graph (:func:`generate_graphed`). ``max_cache_len``
     (a power of two in [16, 2^20]) bounds prompt plus generated tokens. Decode steps on the kernel
     attend to the first ``length`` positions of each buffer and read no attention mask, so a call

@@ -519,3 +519,58 @@ def test_gpu_graphed_generation_quantized(fmt, monkeypatch):
         if a != b:
             assert margins[i] < 2e-2, ("divergence at step %d without a tie" % i, margins[i])
             break
+
+
+@pytest.mark.gpu
+def test_gpu_bf16_model_decodes_on_the_kernel(monkeypatch):
+    """A bf16 model: decode steps read the bf16 cache in place (decode_attn_gqa_strided, no
+    conversion of the cache). Attention level: the hook's output on layer 0's bf16 cache equals
+    float32 attention over it (max-abs 4e-3 relative to the output scale: the kernel's 2e-3 plus
+    the bf16 rounding of the result, 2^-9 relative). Model level: the step's logits match SDPA's to 5 % of the logit
+    scale (bf16 SDPA rounds its softmax weights to bf16; the kernel keeps them to 2^-16). Over a
+    static cache the graph-replayed tokens equal the eager steps bit for bit, with the paged kernel
+    in every layer."""
+    import fqkv_decode
+
+    name = hf_llama.register()
+    model = tiny_llama(layers=2, dtype=torch.bfloat16, device="cuda")
+    ids = torch.randint(0, 1000, (2, 300), generator=torch.Generator().manual_seed(13)).cuda()
+    calls = {"strided": 0, "paged": 0}
+    real_s, real_p = fqkv_decode.decode_attn_gqa_strided, fqkv_decode.decode_attn_gqa_paged
+
+    def strided(*a, **k):
+        assert a[1].dtype == torch.bfloat16
+        calls["strided"] += 1
+        return real_s(*a, **k)
+
+    def paged(*a, **k):
+        assert a[1].dtype == torch.bfloat16
+        calls["paged"] += 1
+        return real_p(*a, **k)
+
+    monkeypatch.setattr(fqkv_decode, "decode_attn_gqa_strided", strided)
+    monkeypatch.setattr(fqkv_decode, "decode_attn_gqa_paged", paged)
+    logits = {}
+    for impl in ("sdpa", name):
+        set_impl(model, impl)
+        with torch.no_grad():
+            out = model(ids, use_cache=True)
+            nxt = out.logits[:, -1:].argmax(-1)
+            logits[impl] = model(nxt, past_key_values=out.past_key_values, use_cache=True).logits.float()
+    assert calls["strided"] == 2
+    top = float(logits["sdpa"].abs().max())
+    assert float((logits[name] - logits["sdpa"]).abs().max()) <= 0.05 * top
+
+    k, v = out.past_key_values.layers[0].keys, out.past_key_values.layers[0].values  # [2, 2, 301, 64] bf16
+    q = torch.randn(2, 8, 1, 64, device="cuda", generator=torch.Generator(device="cuda").manual_seed(2)).bfloat16()
+    o, _ = hf_llama.attention_forward(model.model.layers[0].self_attn, q, k, v, None, scaling=1 / 8)
+    Kf, Vf = k.float().repeat_interleave(4, 1), v.float().repeat_interleave(4, 1)
+    ref = torch.softmax(q.float() @ Kf.transpose(-1, -2).contiguous() / 8, -1) @ Vf
+    assert o.dtype == torch.bfloat16
+    # bound: the bf16 rounding of the output (2^-9 relative) plus the kernel's own 2e-3
+    assert float((o.float().transpose(1, 2) - ref).abs().max()) <= 4e-3 * max(1.0, float(ref.abs().max()))
+    eager = hf_llama.generate_graphed(model, ids[:1, :45], 20, use_graph=False)
+    n = calls["paged"]
+    graphed = hf_llama.generate_graphed(model, ids[:1, :45], 20)
+    assert n == 19 * 2 and calls["paged"] - n == 2 * 2
+    assert torch.equal(graphed, eager)
