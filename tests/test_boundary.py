@@ -217,6 +217,9 @@ def test_binding_exposes_quantized_and_quantizer_entry_points():
     K = torch.zeros(1, 2, 40, 64, dtype=torch.float16)[:, :, :30]
     with pytest.raises(RuntimeError, match="^cuda"):
         fqkv_decode.decode_attn_gqa_strided(torch.zeros(1, 4, 64, dtype=torch.float16), K, K, 8)
+    Kb = torch.zeros(1, 2, 30, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="^cuda"):
+        fqkv_decode.decode_attn_gqa_strided(torch.zeros(1, 4, 64, dtype=torch.float16), Kb, Kb, 8)
 
 
 def test_capi_layout_entry_points_reject_bad_args(lib):
@@ -237,6 +240,11 @@ def test_capi_layout_entry_points_reject_bad_args(lib):
     assert "null page table" in _err(lib)
     assert fp(*ok, 1, 32, 8, 0, 4, 16, 64, 128, 0, 4096, 256, 2048, 0, 0, 1, 8, None, 0, None) == 1
     assert _err(lib).startswith("pages:")
+    # bf16 (kv_format 3) is a layout format: accepted, so the next check speaks (token stride < 256 B)
+    assert fs(*[16] * 6, 1, 32, 8, 64, 128, 3, 65536, 256, 128, 0, 0, 1, 8, None, 0, None) == 1
+    assert _err(lib).startswith("strides:") and "256" in _err(lib)
+    assert fs(*[16] * 6, 1, 32, 8, 64, 128, 4, 65536, 256, 256, 0, 0, 1, 8, None, 0, None) == 1
+    assert "kv_format" in _err(lib)
 
 
 def test_capi_probes_reject_bad_args(lib):
