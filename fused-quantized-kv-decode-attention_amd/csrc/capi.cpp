@@ -736,9 +736,10 @@ int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, co
   if (tokens < 0 || kv_heads < 1)
     return fail(FQKV_ERR_ARG, "shape: tokens must be >= 0 and kv_heads >= 1, got %lld and %lld", (long long)tokens,
                 (long long)kv_heads);
-  if (num_pages < 1 || page_size < 1 || (page_size & (page_size - 1)) || page_size > (1 << 30))
-    return fail(FQKV_ERR_ARG, "page: num_pages must be >= 1 and page_size a power of two, got %lld and %lld",
-                (long long)num_pages, (long long)page_size);
+  if (num_pages < 1 || page_size < 1 || (page_size & (page_size - 1)) || page_size > (1 << 30) ||
+      num_pages > (INT64_MAX >> 31))
+    return fail(FQKV_ERR_ARG, "page: num_pages must be in [1, 2^32) and page_size a power of two <= 2^30, got %lld "
+                "and %lld", (long long)num_pages, (long long)page_size);
   const int64_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
   if (page_stride < 0 || token_stride < 0 || head_stride < 0 || page_stride % qal || token_stride % qal ||
       head_stride % qal)
