@@ -650,17 +650,17 @@ int fqkv_quantize_kv(const void* X, int x_dtype, void* Q, void* scales, int64_t 
                      int kv_format, void* stream) {
   if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
     return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
-  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32)
-    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16 or FQKV_SRC_F32");
+  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32 && x_dtype != FQKV_SRC_BF16)
+    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16, FQKV_SRC_F32 or FQKV_SRC_BF16");
   if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
   if (tokens < 1) return fail(FQKV_ERR_ARG, "tokens must be >= 1, got %lld", (long long)tokens);
   if (!X || !Q || !scales) return fail(FQKV_ERR_ARG, "null tensor pointer");
-  const uintptr_t xal = (x_dtype == FQKV_SRC_F16 && D == 64) ? 8 : 16;
+  const uintptr_t xal = (x_dtype != FQKV_SRC_F32 && D == 64) ? 8 : 16;
   const uintptr_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
   if (!aligned(X, xal)) return fail(FQKV_ERR_ARG, "X must be %d-byte aligned", (int)xal);
   if (!aligned(Q, qal)) return fail(FQKV_ERR_ARG, "Q must be %d-byte aligned", (int)qal);
   if (!aligned(scales, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
-  hipError_t e = launch_quantize(x_dtype == FQKV_SRC_F16, kv_format, (int)D, X, Q, scales, tokens,
+  hipError_t e = launch_quantize(x_dtype, kv_format, (int)D, X, Q, scales, tokens,
                                  (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "launch: quantize kernel");
   return FQKV_OK;
@@ -671,8 +671,8 @@ int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, v
                             int64_t pos, int64_t D, int kv_format, void* stream) {
   if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
     return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
-  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32)
-    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16 or FQKV_SRC_F32");
+  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32 && x_dtype != FQKV_SRC_BF16)
+    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16, FQKV_SRC_F32 or FQKV_SRC_BF16");
   if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
   if (rows < 1 || n_new < 1) return fail(FQKV_ERR_ARG, "rows and n_new must be >= 1, got %lld and %lld",
                                          (long long)rows, (long long)n_new);
@@ -680,12 +680,12 @@ int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, v
     return fail(FQKV_ERR_ARG, "pos: tokens %lld .. %lld do not fit a capacity of %lld", (long long)pos,
                 (long long)(pos + n_new - 1), (long long)capacity);
   if (!K_new || !V_new || !K_cache || !V_cache || !Ks_cache || !Vs_cache) return fail(FQKV_ERR_ARG, "null tensor pointer");
-  const uintptr_t xal = (x_dtype == FQKV_SRC_F16 && D == 64) ? 8 : 16;
+  const uintptr_t xal = (x_dtype != FQKV_SRC_F32 && D == 64) ? 8 : 16;
   const uintptr_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
   if (!aligned(K_new, xal) || !aligned(V_new, xal)) return fail(FQKV_ERR_ARG, "K_new and V_new must be %d-byte aligned", (int)xal);
   if (!aligned(K_cache, qal) || !aligned(V_cache, qal)) return fail(FQKV_ERR_ARG, "caches must be %d-byte aligned", (int)qal);
   if (!aligned(Ks_cache, 2) || !aligned(Vs_cache, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
-  hipError_t e = launch_quantize_append(x_dtype == FQKV_SRC_F16, kv_format, (int)D, K_new, V_new, K_cache, V_cache,
+  hipError_t e = launch_quantize_append(x_dtype, kv_format, (int)D, K_new, V_new, K_cache, V_cache,
                                         Ks_cache, Vs_cache, rows, n_new, capacity, pos, nullptr, 1,
                                         (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "launch: quantize append kernel");
@@ -697,8 +697,8 @@ int fqkv_quantize_kv_append_at(const void* K_new, const void* V_new, int x_dtype
                                const int32_t* pos, int64_t rows_per_pos, int64_t D, int kv_format, void* stream) {
   if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
     return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
-  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32)
-    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16 or FQKV_SRC_F32");
+  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32 && x_dtype != FQKV_SRC_BF16)
+    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16, FQKV_SRC_F32 or FQKV_SRC_BF16");
   if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
   if (rows < 1 || n_new < 1) return fail(FQKV_ERR_ARG, "rows and n_new must be >= 1, got %lld and %lld",
                                          (long long)rows, (long long)n_new);
@@ -710,13 +710,13 @@ int fqkv_quantize_kv_append_at(const void* K_new, const void* V_new, int x_dtype
                 (long long)rows);
   if (!K_new || !V_new || !K_cache || !V_cache || !Ks_cache || !Vs_cache || !pos)
     return fail(FQKV_ERR_ARG, "null tensor pointer");
-  const uintptr_t xal = (x_dtype == FQKV_SRC_F16 && D == 64) ? 8 : 16;
+  const uintptr_t xal = (x_dtype != FQKV_SRC_F32 && D == 64) ? 8 : 16;
   const uintptr_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
   if (!aligned(K_new, xal) || !aligned(V_new, xal)) return fail(FQKV_ERR_ARG, "K_new and V_new must be %d-byte aligned", (int)xal);
   if (!aligned(K_cache, qal) || !aligned(V_cache, qal)) return fail(FQKV_ERR_ARG, "caches must be %d-byte aligned", (int)qal);
   if (!aligned(Ks_cache, 2) || !aligned(Vs_cache, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
   if (!aligned(pos, 4)) return fail(FQKV_ERR_ARG, "pos must be 4-byte aligned");
-  hipError_t e = launch_quantize_append(x_dtype == FQKV_SRC_F16, kv_format, (int)D, K_new, V_new, K_cache, V_cache,
+  hipError_t e = launch_quantize_append(x_dtype, kv_format, (int)D, K_new, V_new, K_cache, V_cache,
                                         Ks_cache, Vs_cache, rows, n_new, capacity, 0, pos, rows_per_pos,
                                         (hipStream_t)stream);
   if (e != hipSuccess) return hip_fail(e, "launch: quantize append kernel");
@@ -730,8 +730,8 @@ int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, co
                            int64_t s_token_stride, int64_t s_head_stride, int kv_format, void* stream) {
   if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
     return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
-  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32)
-    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16 or FQKV_SRC_F32");
+  if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32 && x_dtype != FQKV_SRC_BF16)
+    return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16, FQKV_SRC_F32 or FQKV_SRC_BF16");
   if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
   if (tokens < 0 || kv_heads < 1)
     return fail(FQKV_ERR_ARG, "shape: tokens must be >= 0 and kv_heads >= 1, got %lld and %lld", (long long)tokens,
@@ -748,7 +748,7 @@ int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, co
     return fail(FQKV_ERR_ARG, "stride: scale strides must be non-negative");
   if (!K_new || !V_new || !slot_mapping || !K_pages || !V_pages || !Ks_pages || !Vs_pages)
     return fail(FQKV_ERR_ARG, "null tensor pointer");
-  const uintptr_t xal = (x_dtype == FQKV_SRC_F16 && D == 64) ? 8 : 16;
+  const uintptr_t xal = (x_dtype != FQKV_SRC_F32 && D == 64) ? 8 : 16;
   if (!aligned(K_new, xal) || !aligned(V_new, xal)) return fail(FQKV_ERR_ARG, "K_new and V_new must be %d-byte aligned", (int)xal);
   if (!aligned(K_pages, (uintptr_t)qal) || !aligned(V_pages, (uintptr_t)qal))
     return fail(FQKV_ERR_ARG, "pages must be %d-byte aligned", (int)qal);
@@ -756,7 +756,7 @@ int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, co
   if (!aligned(slot_mapping, 4)) return fail(FQKV_ERR_ARG, "slot_mapping must be 4-byte aligned");
   if (tokens == 0) return FQKV_OK;
   const int page_log2 = __builtin_ctzll((unsigned long long)page_size);
-  hipError_t e = launch_quantize_pages(x_dtype == FQKV_SRC_F16, kv_format, (int)D, K_new, V_new, slot_mapping, tokens,
+  hipError_t e = launch_quantize_pages(x_dtype, kv_format, (int)D, K_new, V_new, slot_mapping, tokens,
                                        kv_heads, K_pages, V_pages, Ks_pages, Vs_pages, num_pages, page_log2,
                                        page_stride, token_stride, head_stride, s_page_stride, s_token_stride,
                                        s_head_stride, (hipStream_t)stream);

@@ -114,12 +114,12 @@ hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* sink, int
 hipError_t launch_buffer_range(const void* buf, int records, uint32_t* out, hipStream_t st);
 // Measurement knob: P.V of fp16, D 128, 1 or 4 heads per group, contiguous rows on the vector ALUs.
 void set_pv_valu(int on);
-hipError_t launch_quantize(int src_f16, int fmt, int D, const void* X, void* Q, void* S, int64_t tokens,
+hipError_t launch_quantize(int src, int fmt, int D, const void* X, void* Q, void* S, int64_t tokens,
                            hipStream_t st);
-hipError_t launch_quantize_append(int src_f16, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,
+hipError_t launch_quantize_append(int src, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,
                                   void* Sk, void* Sv, int64_t rows, int64_t n, int64_t cap, int64_t pos,
                                   const int32_t* pos_of, int64_t rows_per_pos, hipStream_t st);
-hipError_t launch_quantize_pages(int src_f16, int fmt, int D, const void* Xk, const void* Xv, const int32_t* slots,
+hipError_t launch_quantize_pages(int src, int fmt, int D, const void* Xk, const void* Xv, const int32_t* slots,
                                  int64_t tokens, int64_t heads, void* Qk, void* Qv, void* Sk, void* Sv,
                                  int64_t num_pages, int page_log2, int64_t q_page, int64_t q_tok, int64_t q_head,
                                  int64_t s_page, int64_t s_tok, int64_t s_head, hipStream_t st);

@@ -29,6 +29,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "kv_formats.h"
 #include "launch.h"
 
@@ -49,9 +51,28 @@ __device__ __forceinline__ float row16_max(float x) {
   return fmaxf(x, dpp_f<0x140>(x));
 }
 
-template <bool F16, int EPL>
+// Source element types (the public header's FQKV_SRC_* values). bf16 rows
+// widen exactly to fp32 and then follow the fp32 expressions.
+enum { SRC_F16 = 0, SRC_F32 = 1, SRC_BF16 = 2 };
+
+template <int SRC, int EPL>
 __device__ __forceinline__ void load_row_slice(const void* X, int64_t row, int i, int D, float (&x)[EPL]) {
-  if constexpr (F16) {
+  if constexpr (SRC == SRC_BF16) {
+    const uint16_t* p = (const uint16_t*)X + row * D + EPL * i;
+    uint32_t w[EPL / 2];
+    if constexpr (EPL == 8) {
+      const u4_t v = *(const u4_t*)p;
+      w[0] = v.x, w[1] = v.y, w[2] = v.z, w[3] = v.w;
+    } else {
+      const u2_t v = *(const u2_t*)p;
+      w[0] = v.x, w[1] = v.y;
+    }
+#pragma unroll
+    for (int k = 0; k < EPL / 2; ++k) {
+      x[2 * k] = __builtin_bit_cast(float, w[k] << 16);
+      x[2 * k + 1] = __builtin_bit_cast(float, w[k] & 0xFFFF0000u);
+    }
+  } else if constexpr (SRC == SRC_F16) {
     const _Float16* p = (const _Float16*)X + row * D + EPL * i;
     if constexpr (EPL == 8) {
       const h8_t v = *(const h8_t*)p;
@@ -87,13 +108,14 @@ __device__ __forceinline__ void load_row_slice(const void* X, int64_t row, int i
 // bytes or D/2 packed int4 bytes) and its scale at *srow. The calling 16
 // lanes stay active together (the DPP reduction spans them); a group with
 // live == false reads and writes nothing (its pointers may be anything).
-template <bool F16, int QMAX, int D>
+template <int SRC, int QMAX, int D>
 __device__ __forceinline__ void quantize_row(const void* __restrict__ X, int64_t row, uint8_t* __restrict__ qrow,
                                              _Float16* __restrict__ srow, bool live, int i) {
+  constexpr bool F16 = SRC == SRC_F16;  // fp16 rounding of the scale and the quotients
   constexpr int EPL = D / 16;  // elements per lane
   float x[EPL];
   if (live) {
-    load_row_slice<F16, EPL>(X, row, i, D, x);
+    load_row_slice<SRC, EPL>(X, row, i, D, x);
   } else {
 #pragma unroll
     for (int e = 0; e < EPL; ++e) x[e] = 0.0f;
@@ -173,14 +195,14 @@ __device__ __forceinline__ uint8_t* code_row(uint8_t* Q, int64_t dst) {
   return Q + dst * (QMAX == 127 ? D : D / 2);
 }
 
-template <bool F16, int QMAX, int D>
+template <int SRC, int QMAX, int D>
 __global__ void __launch_bounds__(256) quantize_kernel(const void* __restrict__ X, uint8_t* __restrict__ Q,
                                                        _Float16* __restrict__ scales, int64_t tokens) {
   const int i = threadIdx.x & 15;
   const int64_t rows_per_step = (int64_t)gridDim.x * (blockDim.x >> 4);
   for (int64_t row = (int64_t)blockIdx.x * (blockDim.x >> 4) + (threadIdx.x >> 4);
        row - (threadIdx.x >> 4) < tokens; row += rows_per_step)
-    quantize_row<F16, QMAX, D>(X, row, code_row<QMAX, D>(Q, row), scales + row, row < tokens, i);
+    quantize_row<SRC, QMAX, D>(X, row, code_row<QMAX, D>(Q, row), scales + row, row < tokens, i);
 }
 
 // Append form for a live cache: K and V rows of `rows` cache rows x n new
@@ -190,7 +212,7 @@ __global__ void __launch_bounds__(256) quantize_kernel(const void* __restrict__ 
 // the position of cache row r is pos_of[r / rows_per_pos] instead, read on the
 // device (so a captured graph appends where the cache currently ends); rows
 // whose tokens would not fit in [0, cap) are not written.
-template <bool F16, int QMAX, int D>
+template <int SRC, int QMAX, int D>
 __global__ void __launch_bounds__(256) quantize_append_kernel(const void* __restrict__ Xk, const void* __restrict__ Xv,
                                                               uint8_t* __restrict__ Qk, uint8_t* __restrict__ Qv,
                                                               _Float16* __restrict__ Sk, _Float16* __restrict__ Sv,
@@ -211,7 +233,7 @@ __global__ void __launch_bounds__(256) quantize_append_kernel(const void* __rest
       fits = p >= 0 && p <= cap - n;
     }
     const int64_t dst = r * cap + (fits ? p : 0) + (row - r * n);
-    quantize_row<F16, QMAX, D>(v ? Xv : Xk, row, code_row<QMAX, D>(v ? Qv : Qk, dst), (v ? Sv : Sk) + dst, in && fits,
+    quantize_row<SRC, QMAX, D>(v ? Xv : Xk, row, code_row<QMAX, D>(v ? Qv : Qk, dst), (v ? Sv : Sk) + dst, in && fits,
                                i);
   }
 }
@@ -230,7 +252,7 @@ struct PagedDst {
   int page_log2;
 };
 
-template <bool F16, int QMAX, int D>
+template <int SRC, int QMAX, int D>
 __global__ void __launch_bounds__(256) quantize_pages_kernel(const void* __restrict__ Xk, const void* __restrict__ Xv,
                                                              const int32_t* __restrict__ slots, int64_t rows,
                                                              int64_t heads, PagedDst d) {
@@ -247,50 +269,50 @@ __global__ void __launch_bounds__(256) quantize_pages_kernel(const void* __restr
     const bool live = slot >= 0 && slot < d.nslots;
     const int64_t pg = live ? slot >> d.page_log2 : 0;
     const int64_t off = live ? slot - (pg << d.page_log2) : 0;
-    quantize_row<F16, QMAX, D>(v ? Xv : Xk, row, d.q[v] + pg * d.q_page + off * d.q_tok + h * d.q_head,
+    quantize_row<SRC, QMAX, D>(v ? Xv : Xk, row, d.q[v] + pg * d.q_page + off * d.q_tok + h * d.q_head,
                                d.s[v] + pg * d.s_page + off * d.s_tok + h * d.s_head, live, i);
   }
 }
 
-template <bool F16, int QMAX>
+template <int SRC, int QMAX>
 hipError_t launch_qp(int D, const void* Xk, const void* Xv, const int32_t* slots, int64_t rows, int64_t heads,
                      const PagedDst& d, hipStream_t st) {
   const int64_t want = (2 * rows + 15) / 16;
   const unsigned grid = (unsigned)(want < (1 << 16) ? want : (1 << 16));
   if (D == 128)
-    hipLaunchKernelGGL((quantize_pages_kernel<F16, QMAX, 128>), dim3(grid), dim3(256), 0, st, Xk, Xv, slots, rows,
+    hipLaunchKernelGGL((quantize_pages_kernel<SRC, QMAX, 128>), dim3(grid), dim3(256), 0, st, Xk, Xv, slots, rows,
                        heads, d);
   else
-    hipLaunchKernelGGL((quantize_pages_kernel<F16, QMAX, 64>), dim3(grid), dim3(256), 0, st, Xk, Xv, slots, rows,
+    hipLaunchKernelGGL((quantize_pages_kernel<SRC, QMAX, 64>), dim3(grid), dim3(256), 0, st, Xk, Xv, slots, rows,
                        heads, d);
   return hipGetLastError();
 }
 
-template <bool F16, int QMAX>
+template <int SRC, int QMAX>
 hipError_t launch_q(int D, const void* X, void* Q, void* S, int64_t tokens, hipStream_t st) {
   const int64_t want = (tokens + 15) / 16;
   const unsigned grid = (unsigned)(want < (1 << 16) ? want : (1 << 16));
   if (D == 128)
-    hipLaunchKernelGGL((quantize_kernel<F16, QMAX, 128>), dim3(grid), dim3(256), 0, st, X, (uint8_t*)Q,
+    hipLaunchKernelGGL((quantize_kernel<SRC, QMAX, 128>), dim3(grid), dim3(256), 0, st, X, (uint8_t*)Q,
                        (_Float16*)S, tokens);
   else
-    hipLaunchKernelGGL((quantize_kernel<F16, QMAX, 64>), dim3(grid), dim3(256), 0, st, X, (uint8_t*)Q,
+    hipLaunchKernelGGL((quantize_kernel<SRC, QMAX, 64>), dim3(grid), dim3(256), 0, st, X, (uint8_t*)Q,
                        (_Float16*)S, tokens);
   return hipGetLastError();
 }
 
-template <bool F16, int QMAX>
+template <int SRC, int QMAX>
 hipError_t launch_qa(int D, const void* Xk, const void* Xv, void* Qk, void* Qv, void* Sk, void* Sv, int64_t tokens,
                      int64_t n, int64_t cap, int64_t pos, const int32_t* pos_of, int64_t rows_per_pos,
                      hipStream_t st) {
   const int64_t want = (2 * tokens + 15) / 16;
   const unsigned grid = (unsigned)(want < (1 << 16) ? want : (1 << 16));
   if (D == 128)
-    hipLaunchKernelGGL((quantize_append_kernel<F16, QMAX, 128>), dim3(grid), dim3(256), 0, st, Xk, Xv,
+    hipLaunchKernelGGL((quantize_append_kernel<SRC, QMAX, 128>), dim3(grid), dim3(256), 0, st, Xk, Xv,
                        (uint8_t*)Qk, (uint8_t*)Qv, (_Float16*)Sk, (_Float16*)Sv, tokens, n, cap, pos, pos_of,
                        rows_per_pos);
   else
-    hipLaunchKernelGGL((quantize_append_kernel<F16, QMAX, 64>), dim3(grid), dim3(256), 0, st, Xk, Xv,
+    hipLaunchKernelGGL((quantize_append_kernel<SRC, QMAX, 64>), dim3(grid), dim3(256), 0, st, Xk, Xv,
                        (uint8_t*)Qk, (uint8_t*)Qv, (_Float16*)Sk, (_Float16*)Sv, tokens, n, cap, pos, pos_of,
                        rows_per_pos);
   return hipGetLastError();
@@ -298,23 +320,36 @@ hipError_t launch_qa(int D, const void* Xk, const void* Xv, void* Qk, void* Qv, 
 
 }  // namespace
 
-hipError_t launch_quantize_append(int src_f16, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,
+// A launcher templated on <SRC, QMAX> for run-time source type and format.
+template <typename Fn>
+hipError_t by_src_fmt(int src, int fmt, Fn f) {
+  auto q = [&](auto src_c) -> hipError_t {
+    if (fmt == KV_I8) return f(src_c, std::integral_constant<int, 127>());
+    if (fmt == KV_I4) return f(src_c, std::integral_constant<int, 7>());
+    return hipErrorInvalidValue;
+  };
+  switch (src) {
+    case SRC_F16: return q(std::integral_constant<int, SRC_F16>());
+    case SRC_F32: return q(std::integral_constant<int, SRC_F32>());
+    case SRC_BF16: return q(std::integral_constant<int, SRC_BF16>());
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_quantize_append(int src, int fmt, int D, const void* Xk, const void* Xv, void* Qk, void* Qv,
                                   void* Sk, void* Sv, int64_t rows, int64_t n, int64_t cap, int64_t pos,
                                   const int32_t* pos_of, int64_t rows_per_pos, hipStream_t st) {
   if (rows < 1 || n < 1 || cap < 1 || n > cap || (D != 64 && D != 128)) return hipErrorInvalidValue;
   if (pos_of ? (rows_per_pos < 1 || rows % rows_per_pos != 0) : (pos < 0 || pos + n > cap))
     return hipErrorInvalidValue;
   const int64_t tokens = rows * n;
-  if (fmt == KV_I8)
-    return src_f16 ? launch_qa<true, 127>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st)
-                   : launch_qa<false, 127>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st);
-  if (fmt == KV_I4)
-    return src_f16 ? launch_qa<true, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st)
-                   : launch_qa<false, 7>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos, pos_of, rows_per_pos, st);
-  return hipErrorInvalidValue;
+  return by_src_fmt(src, fmt, [&](auto s_c, auto q_c) {
+    return launch_qa<decltype(s_c)::value, decltype(q_c)::value>(D, Xk, Xv, Qk, Qv, Sk, Sv, tokens, n, cap, pos,
+                                                                  pos_of, rows_per_pos, st);
+  });
 }
 
-hipError_t launch_quantize_pages(int src_f16, int fmt, int D, const void* Xk, const void* Xv, const int32_t* slots,
+hipError_t launch_quantize_pages(int src, int fmt, int D, const void* Xk, const void* Xv, const int32_t* slots,
                                  int64_t tokens, int64_t heads, void* Qk, void* Qv, void* Sk, void* Sv,
                                  int64_t num_pages, int page_log2, int64_t q_page, int64_t q_tok, int64_t q_head,
                                  int64_t s_page, int64_t s_tok, int64_t s_head, hipStream_t st) {
@@ -334,21 +369,17 @@ hipError_t launch_quantize_pages(int src_f16, int fmt, int D, const void* Xk, co
   d.nslots = num_pages << page_log2;
   d.page_log2 = page_log2;
   const int64_t rows = tokens * heads;
-  if (fmt == KV_I8)
-    return src_f16 ? launch_qp<true, 127>(D, Xk, Xv, slots, rows, heads, d, st)
-                   : launch_qp<false, 127>(D, Xk, Xv, slots, rows, heads, d, st);
-  if (fmt == KV_I4)
-    return src_f16 ? launch_qp<true, 7>(D, Xk, Xv, slots, rows, heads, d, st)
-                   : launch_qp<false, 7>(D, Xk, Xv, slots, rows, heads, d, st);
-  return hipErrorInvalidValue;
+  return by_src_fmt(src, fmt, [&](auto s_c, auto q_c) {
+    return launch_qp<decltype(s_c)::value, decltype(q_c)::value>(D, Xk, Xv, slots, rows, heads, d, st);
+  });
 }
 
-hipError_t launch_quantize(int src_f16, int fmt, int D, const void* X, void* Q, void* S, int64_t tokens,
+hipError_t launch_quantize(int src, int fmt, int D, const void* X, void* Q, void* S, int64_t tokens,
                            hipStream_t st) {
   if (tokens < 1 || (D != 64 && D != 128)) return hipErrorInvalidValue;
-  if (fmt == KV_I8) return src_f16 ? launch_q<true, 127>(D, X, Q, S, tokens, st) : launch_q<false, 127>(D, X, Q, S, tokens, st);
-  if (fmt == KV_I4) return src_f16 ? launch_q<true, 7>(D, X, Q, S, tokens, st) : launch_q<false, 7>(D, X, Q, S, tokens, st);
-  return hipErrorInvalidValue;
+  return by_src_fmt(src, fmt, [&](auto s_c, auto q_c) {
+    return launch_q<decltype(s_c)::value, decltype(q_c)::value>(D, X, Q, S, tokens, st);
+  });
 }
 
 }  // namespace fqkv

@@ -50,6 +50,16 @@ void check_W(int64_t W) { TORCH_CHECK(W == 2 || W == 4 || W == 8, "W: must be 2,
 
 void check_D(int64_t D) { TORCH_CHECK(D == 64 || D == 128, "D: head_dim must be 64 or 128, got ", D); }
 
+// Quantizer source element type (FQKV_SRC_*), -1 for any other dtype.
+int src_of(const torch::Tensor& X) {
+  switch (X.scalar_type()) {
+    case torch::kHalf: return FQKV_SRC_F16;
+    case torch::kFloat: return FQKV_SRC_F32;
+    case torch::kBFloat16: return FQKV_SRC_BF16;
+    default: return -1;
+  }
+}
+
 torch::Tensor workspace_for(const torch::Tensor& q, int64_t rows, int64_t G, int64_t N, int64_t D,
                             int fmt, int64_t W) {
   const c10::DeviceGuard guard(q.device());
@@ -506,8 +516,8 @@ int64_t cu_count() {
 // PyTorch expressions (tests/test_kernels.py:32-34, nb:292-299).
 static std::vector<torch::Tensor> quantize_per_token(torch::Tensor X, int fmt) {
   check_gpu({&X});
-  TORCH_CHECK(X.scalar_type() == torch::kHalf || X.scalar_type() == torch::kFloat,
-              "fp16: X must be float16 or float32");
+  TORCH_CHECK(src_of(X) >= 0,
+              "fp16: X must be float16, float32 or bfloat16");
   TORCH_CHECK(X.is_contiguous(), "contig: X must be contiguous");
   TORCH_CHECK(X.dim() >= 1, "shape: X must be [..., D]");
   const int64_t D = X.size(-1);
@@ -521,7 +531,7 @@ static std::vector<torch::Tensor> quantize_per_token(torch::Tensor X, int fmt) {
   auto ssizes = X.sizes().vec();
   ssizes.pop_back();
   auto S = torch::empty(ssizes, X.options().dtype(torch::kHalf));
-  check_rc(fqkv_quantize_kv(X.data_ptr(), X.scalar_type() == torch::kHalf ? FQKV_SRC_F16 : FQKV_SRC_F32,
+  check_rc(fqkv_quantize_kv(X.data_ptr(), src_of(X),
                             Q.data_ptr(), S.data_ptr(), tokens, D, fmt, cur_stream(X)),
            "launch");
   return {Q, S};
@@ -539,8 +549,8 @@ static std::vector<torch::Tensor> quantize_int4_per_token(torch::Tensor X) {
 static void quantize_kv_append(torch::Tensor Kn, torch::Tensor Vn, torch::Tensor Kc, torch::Tensor Vc,
                                torch::Tensor Ksc, torch::Tensor Vsc, int64_t pos) {
   check_gpu({&Kn, &Vn, &Kc, &Vc, &Ksc, &Vsc});
-  TORCH_CHECK(Kn.scalar_type() == torch::kHalf || Kn.scalar_type() == torch::kFloat,
-              "fp16: K_new must be float16 or float32");
+  TORCH_CHECK(src_of(Kn) >= 0,
+              "fp16: K_new must be float16, float32 or bfloat16");
   TORCH_CHECK(Vn.scalar_type() == Kn.scalar_type() && Vn.sizes() == Kn.sizes() && Kn.dim() == 4,
               "shape: K_new and V_new must be [B,H,n,D] of one dtype; got ", Kn.sizes(), " and ", Vn.sizes());
   TORCH_CHECK(Kc.scalar_type() == torch::kChar || Kc.scalar_type() == torch::kByte,
@@ -560,7 +570,7 @@ static void quantize_kv_append(torch::Tensor Kn, torch::Tensor Vn, torch::Tensor
               Vsc.sizes());
   const c10::DeviceGuard guard(Kn.device());
   check_rc(fqkv_quantize_kv_append(Kn.data_ptr(), Vn.data_ptr(),
-                                   Kn.scalar_type() == torch::kHalf ? FQKV_SRC_F16 : FQKV_SRC_F32, Kc.data_ptr(),
+                                   src_of(Kn), Kc.data_ptr(),
                                    Vc.data_ptr(), Ksc.data_ptr(), Vsc.data_ptr(), B * H, n, cap, pos, D, fmt,
                                    cur_stream(Kn)),
            "launch");
@@ -572,8 +582,8 @@ static void quantize_kv_append(torch::Tensor Kn, torch::Tensor Vn, torch::Tensor
 static void quantize_kv_append_at(torch::Tensor Kn, torch::Tensor Vn, torch::Tensor Kc, torch::Tensor Vc,
                                   torch::Tensor Ksc, torch::Tensor Vsc, torch::Tensor pos) {
   check_gpu({&Kn, &Vn, &Kc, &Vc, &Ksc, &Vsc, &pos});
-  TORCH_CHECK(Kn.scalar_type() == torch::kHalf || Kn.scalar_type() == torch::kFloat,
-              "fp16: K_new must be float16 or float32");
+  TORCH_CHECK(src_of(Kn) >= 0,
+              "fp16: K_new must be float16, float32 or bfloat16");
   TORCH_CHECK(Vn.scalar_type() == Kn.scalar_type() && Vn.sizes() == Kn.sizes() && Kn.dim() == 4,
               "shape: K_new and V_new must be [B,H,n,D] of one dtype; got ", Kn.sizes(), " and ", Vn.sizes());
   TORCH_CHECK(Kc.scalar_type() == torch::kChar || Kc.scalar_type() == torch::kByte,
@@ -595,7 +605,7 @@ static void quantize_kv_append_at(torch::Tensor Kn, torch::Tensor Vn, torch::Ten
               "shape: pos must be int32 [B] = [", B, "], contiguous");
   const c10::DeviceGuard guard(Kn.device());
   check_rc(fqkv_quantize_kv_append_at(Kn.data_ptr(), Vn.data_ptr(),
-                                      Kn.scalar_type() == torch::kHalf ? FQKV_SRC_F16 : FQKV_SRC_F32, Kc.data_ptr(),
+                                      src_of(Kn), Kc.data_ptr(),
                                       Vc.data_ptr(), Ksc.data_ptr(), Vsc.data_ptr(), B * H, n, cap,
                                       pos.data_ptr<int32_t>(), H, D, fmt, cur_stream(Kn)),
            "launch");
@@ -610,8 +620,8 @@ static void quantize_kv_to_pages(torch::Tensor Kn, torch::Tensor Vn, torch::Tens
                                  torch::Tensor Vp, torch::Tensor Ksp, torch::Tensor Vsp) {
   check_gpu({&Kn, &Vn, &slots});
   check_gpu_strided({&Kp, &Vp, &Ksp, &Vsp}, Kn);
-  TORCH_CHECK(Kn.scalar_type() == torch::kHalf || Kn.scalar_type() == torch::kFloat,
-              "fp16: K_new must be float16 or float32");
+  TORCH_CHECK(src_of(Kn) >= 0,
+              "fp16: K_new must be float16, float32 or bfloat16");
   TORCH_CHECK(Kn.dim() == 3 && Vn.sizes() == Kn.sizes() && Vn.scalar_type() == Kn.scalar_type(),
               "shape: K_new and V_new must be [T,Hkv,D] of one dtype; got ", Kn.sizes(), " and ", Vn.sizes());
   TORCH_CHECK(Kp.scalar_type() == torch::kChar || Kp.scalar_type() == torch::kByte,
@@ -633,7 +643,7 @@ static void quantize_kv_to_pages(torch::Tensor Kn, torch::Tensor Vn, torch::Tens
               "shape: slot_mapping must be int32 [T] = [", T, "]");
   const c10::DeviceGuard guard(Kn.device());
   check_rc(fqkv_quantize_kv_paged(Kn.data_ptr(), Vn.data_ptr(),
-                                  Kn.scalar_type() == torch::kHalf ? FQKV_SRC_F16 : FQKV_SRC_F32,
+                                  src_of(Kn),
                                   slots.data_ptr<int32_t>(), T, H, D, Kp.data_ptr(), Vp.data_ptr(), Ksp.data_ptr(),
                                   Vsp.data_ptr(), Kp.size(0), Kp.size(1), Kp.stride(0), Kp.stride(1), Kp.stride(2),
                                   Ksp.stride(0), Ksp.stride(1), Ksp.stride(2), fmt, cur_stream(Kn)),

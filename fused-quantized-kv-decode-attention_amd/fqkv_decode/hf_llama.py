@@ -221,7 +221,8 @@ def _make_layer_class():
             B, H, n, D = key_states.shape
             first = self.length == 0
             self._reserve(B, H, D, self.length + n)
-            src = (lambda t: t) if key_states.dtype in (torch.float16, torch.float32) else (lambda t: t.float())
+            src = (lambda t: t) if key_states.dtype in (torch.float16, torch.float32, torch.bfloat16) else (
+                lambda t: t.float())
             # one launch quantizes the new K and V tokens into their cache slots
             quantize_kv_append_(src(key_states).contiguous(), src(value_states).contiguous(), self._k, self._v,
                                 self._ks, self._vs, self.length)
@@ -397,7 +398,7 @@ def _make_static_layer_class():
             if not self.is_initialized:
                 self.lazy_initialization(key_states, value_states)
             kn, vn = key_states, value_states
-            if kn.dtype not in (torch.float16, torch.float32):
+            if kn.dtype not in (torch.float16, torch.float32, torch.bfloat16):
                 kn, vn = kn.float(), vn.float()
             # one launch quantizes the new K and V tokens into their slots, at seq_lens on the device
             quantize_kv_append_at_(kn.contiguous(), vn.contiguous(), self.keys, self.values, self.key_scales,

@@ -59,7 +59,10 @@ enum {
  * points, for caches kept in a bf16 model's own dtype). */
 enum { FQKV_KV_F16 = 0, FQKV_KV_I8 = 1, FQKV_KV_I4 = 2, FQKV_KV_BF16 = 3 };
 
-enum { FQKV_SRC_F16 = 0, FQKV_SRC_F32 = 1 }; /* element type of a quantizer input */
+/* element type of a quantizer input; bf16 rows widen exactly to fp32 and are
+ * quantized as fp32 (no counterpart in the reference, whose quantizers see
+ * fp16 or fp32 tensors) */
+enum { FQKV_SRC_F16 = 0, FQKV_SRC_F32 = 1, FQKV_SRC_BF16 = 2 };
 
 /* Message for the last failing call on this thread ("" if none). */
 const char* fqkv_last_error(void);

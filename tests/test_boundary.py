@@ -134,7 +134,7 @@ def test_capi_quantizer_rejects_bad_args(lib):
     f = lib.fqkv_quantize_kv
     f.argtypes = [VP, ctypes.c_int, VP, VP, I64, I64, ctypes.c_int, VP]
     assert f(16, 0, 16, 16, 4, 128, 0, None) == 1 and "kv_format" in _err(lib)
-    assert f(16, 2, 16, 16, 4, 128, 1, None) == 1 and "x_dtype" in _err(lib)
+    assert f(16, 3, 16, 16, 4, 128, 1, None) == 1 and "x_dtype" in _err(lib)  # 2 is bf16
     assert f(16, 1, 16, 16, 4, 96, 1, None) == 1 and _err(lib).startswith("D:")
     assert f(16, 1, 16, 16, 0, 128, 1, None) == 1 and _err(lib).startswith("tokens")
     assert f(None, 1, 16, 16, 4, 128, 1, None) == 1 and "null" in _err(lib)
@@ -191,7 +191,7 @@ def test_capi_quantize_append_at_rejects_bad_args(lib):
     assert f(*ok, 8, 0, 100, 16, 4, 128, 1, None) == 1 and "n_new" in _err(lib)
     assert f(*ok, 8, 1, 100, 16, 4, 128, 0, None) == 1 and "kv_format" in _err(lib)
     assert f(*ok, 8, 1, 100, 16, 4, 96, 2, None) == 1 and _err(lib).startswith("D:")
-    assert f(16, 16, 2, 16, 16, 16, 16, 8, 1, 100, 16, 4, 128, 1, None) == 1 and "x_dtype" in _err(lib)
+    assert f(16, 16, 3, 16, 16, 16, 16, 8, 1, 100, 16, 4, 128, 1, None) == 1 and "x_dtype" in _err(lib)
 
 
 def test_capi_quantized_gqa_and_split_reject_bad_args(lib):

@@ -194,6 +194,45 @@ def test_gpu_quantize_append_at_device_positions(dtype, D, fmt):
         fq.quantize_kv_append_at_(Kn, Vn, *got, pos.long())
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("fmt", ["int8", "int4"])
+def test_gpu_quantizers_take_bf16_rows(fmt, D):
+    """bf16 rows (a bf16 model's keys and values) widen exactly to fp32, so every quantizer form
+    writes the bytes the fp32 quantizer writes for x.float(): bulk, append at host and device
+    positions, and into pages by slot."""
+    g = torch.Generator().manual_seed(67)
+    qfn = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+    X = (torch.randn(3, 37, D, generator=g) * 5).bfloat16().cuda()
+    X[0, 0] = 0.0  # an all-zero row
+    X[1, 2, 5] = 3.0e38  # beyond fp16's range: exact in bf16 and fp32
+    for got, want in zip(qfn(X), qfn(X.float())):
+        assert torch.equal(got, want)
+    B, H, cap, n = 2, 3, 20, 4
+    width, qdt = (D, torch.int8) if fmt == "int8" else (D // 2, torch.uint8)
+    Kn = (torch.randn(B, H, n, D, generator=g) * 3).bfloat16().cuda()
+    Vn = (torch.randn(B, H, n, D, generator=g) * 3).bfloat16().cuda()
+    for at in (False, True):
+        a = [torch.zeros(B, H, cap, width, dtype=qdt, device="cuda") for _ in range(2)] + \
+            [torch.zeros(B, H, cap, dtype=torch.float16, device="cuda") for _ in range(2)]
+        b = [t.clone() for t in a]
+        if at:
+            pos = torch.tensor([3, 9], dtype=torch.int32, device="cuda")
+            fq.quantize_kv_append_at_(Kn, Vn, *a, pos)
+            fq.quantize_kv_append_at_(Kn.float(), Vn.float(), *b, pos)
+        else:
+            fq.quantize_kv_append_(Kn, Vn, *a, 5)
+            fq.quantize_kv_append_(Kn.float(), Vn.float(), *b, 5)
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+    Kt, Vt = Kn.flatten(0, 2).view(-1, 1, D).expand(-1, H, D).contiguous(), Vn.flatten(0, 2).view(-1, 1, D).expand(-1, H, D).contiguous()
+    slots = torch.randperm(64, generator=g)[:Kt.shape[0]].to(torch.int32).cuda()
+    pa, pb = page_views(4, 16, H, width, qdt, "hnd"), page_views(4, 16, H, width, qdt, "hnd")
+    fq.quantize_kv_to_pages_(Kt, Vt, slots, *pa)
+    fq.quantize_kv_to_pages_(Kt.float(), Vt.float(), slots, *pb)
+    for x, y in zip(pa, pb):
+        assert torch.equal(x, y)
+
+
 def page_views(P, page, H, width, qdt, layout):
     """Sentinel-filled pages [P, page, H, width] and scale pages [P, page, H] as the decode entry point
     takes them: NHD storage as is, HND storage ([P, H, page, .]) through a permuted view."""
