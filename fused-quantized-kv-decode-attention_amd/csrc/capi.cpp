@@ -158,10 +158,10 @@ int check_common(int64_t N, int64_t D, int64_t W) {
 // Single-block style decode: rows KV rows, G query heads per row. Splits the
 // sequence internally when rows alone cannot fill the GPU and the workspace allows.
 int64_t row_bytes_of(int fmt, int64_t D) {
-  return (fmt == KV_F16 || fmt == KV_BF16) ? 2 * D : (fmt == KV_I8 ? D : D / 2);
+  return (fmt == KV_F16 || fmt == KV_BF16) ? 2 * D : (fmt == KV_I4 ? D / 2 : D);
 }
-// int8 / int4: codes with per-token scales
-bool is_quant(int fmt) { return fmt == KV_I8 || fmt == KV_I4; }
+// int8 / int4 / fp8: codes with per-token scales
+bool is_quant(int fmt) { return fmt == KV_I8 || fmt == KV_I4 || fmt == KV_FP8; }
 
 // KV layout of a single-block call (null: the reference's contiguous layout).
 struct Layout {
@@ -512,8 +512,8 @@ int fqkv_decode_attn_gqa_quant(const void* q, const void* K, const void* V, cons
                                const void* Vs, void* o, int64_t B, int64_t Hq, int64_t Hkv, int64_t N,
                                int64_t D, int kv_format, int64_t W, void* workspace,
                                size_t workspace_bytes, void* stream) {
-  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
-    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4 && kv_format != FQKV_KV_FP8)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8, FQKV_KV_I4 or FQKV_KV_FP8");
   int rc = check_common(N, D, W);
   if (rc) return rc;
   if (B < 1) return fail(FQKV_ERR_ARG, "B: batch must be >= 1, got %lld", (long long)B);
@@ -529,8 +529,8 @@ int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const vo
                            float* m_part, float* l_part, float* o_part, void* o, int64_t Hq,
                            int64_t Hkv, int64_t N, int64_t D, int kv_format, int64_t S, int64_t W,
                            int64_t CW, void* stream) {
-  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
-    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4 && kv_format != FQKV_KV_FP8)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8, FQKV_KV_I4 or FQKV_KV_FP8");
   return sk_fast(kv_format, q, K, V, Ks, Vs, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW, stream,
                  nullptr, nullptr);
 }
@@ -538,8 +538,8 @@ int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const vo
 static int check_layout_common(int fmt, int64_t D, const void* q, const void* K, const void* V,
                                const void* Ks, const void* Vs, const void* o, int64_t kv_bs, int64_t kv_hs,
                                int64_t kv_ts, int64_t sc_bs, int64_t sc_hs, int64_t sc_ts) {
-  if (fmt != FQKV_KV_F16 && fmt != FQKV_KV_I8 && fmt != FQKV_KV_I4 && fmt != FQKV_KV_BF16)
-    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_F16, FQKV_KV_BF16, FQKV_KV_I8 or FQKV_KV_I4");
+  if (fmt != FQKV_KV_F16 && fmt != FQKV_KV_I8 && fmt != FQKV_KV_I4 && fmt != FQKV_KV_BF16 && fmt != FQKV_KV_FP8)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_F16, FQKV_KV_BF16, FQKV_KV_I8, FQKV_KV_I4 or FQKV_KV_FP8");
   int rc = !is_quant(fmt) ? check_ptrs_kv(q, K, V, o) : check_ptrs_quant(fmt, D, q, K, V, Ks, Vs, o);
   if (rc) return rc;
   const int64_t rb = row_bytes_of(fmt, D);
@@ -648,15 +648,15 @@ int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, 
 
 int fqkv_quantize_kv(const void* X, int x_dtype, void* Q, void* scales, int64_t tokens, int64_t D,
                      int kv_format, void* stream) {
-  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
-    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4 && kv_format != FQKV_KV_FP8)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8, FQKV_KV_I4 or FQKV_KV_FP8");
   if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32 && x_dtype != FQKV_SRC_BF16)
     return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16, FQKV_SRC_F32 or FQKV_SRC_BF16");
   if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
   if (tokens < 1) return fail(FQKV_ERR_ARG, "tokens must be >= 1, got %lld", (long long)tokens);
   if (!X || !Q || !scales) return fail(FQKV_ERR_ARG, "null tensor pointer");
   const uintptr_t xal = (x_dtype != FQKV_SRC_F32 && D == 64) ? 8 : 16;
-  const uintptr_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
+  const uintptr_t qal = kv_format == FQKV_KV_I4 ? (D == 128 ? 4 : 2) : (D == 128 ? 8 : 4);
   if (!aligned(X, xal)) return fail(FQKV_ERR_ARG, "X must be %d-byte aligned", (int)xal);
   if (!aligned(Q, qal)) return fail(FQKV_ERR_ARG, "Q must be %d-byte aligned", (int)qal);
   if (!aligned(scales, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
@@ -669,8 +669,8 @@ int fqkv_quantize_kv(const void* X, int x_dtype, void* Q, void* scales, int64_t 
 int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, void* K_cache, void* V_cache,
                             void* Ks_cache, void* Vs_cache, int64_t rows, int64_t n_new, int64_t capacity,
                             int64_t pos, int64_t D, int kv_format, void* stream) {
-  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
-    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4 && kv_format != FQKV_KV_FP8)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8, FQKV_KV_I4 or FQKV_KV_FP8");
   if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32 && x_dtype != FQKV_SRC_BF16)
     return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16, FQKV_SRC_F32 or FQKV_SRC_BF16");
   if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
@@ -681,7 +681,7 @@ int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, v
                 (long long)(pos + n_new - 1), (long long)capacity);
   if (!K_new || !V_new || !K_cache || !V_cache || !Ks_cache || !Vs_cache) return fail(FQKV_ERR_ARG, "null tensor pointer");
   const uintptr_t xal = (x_dtype != FQKV_SRC_F32 && D == 64) ? 8 : 16;
-  const uintptr_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
+  const uintptr_t qal = kv_format == FQKV_KV_I4 ? (D == 128 ? 4 : 2) : (D == 128 ? 8 : 4);
   if (!aligned(K_new, xal) || !aligned(V_new, xal)) return fail(FQKV_ERR_ARG, "K_new and V_new must be %d-byte aligned", (int)xal);
   if (!aligned(K_cache, qal) || !aligned(V_cache, qal)) return fail(FQKV_ERR_ARG, "caches must be %d-byte aligned", (int)qal);
   if (!aligned(Ks_cache, 2) || !aligned(Vs_cache, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
@@ -695,8 +695,8 @@ int fqkv_quantize_kv_append(const void* K_new, const void* V_new, int x_dtype, v
 int fqkv_quantize_kv_append_at(const void* K_new, const void* V_new, int x_dtype, void* K_cache, void* V_cache,
                                void* Ks_cache, void* Vs_cache, int64_t rows, int64_t n_new, int64_t capacity,
                                const int32_t* pos, int64_t rows_per_pos, int64_t D, int kv_format, void* stream) {
-  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
-    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4 && kv_format != FQKV_KV_FP8)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8, FQKV_KV_I4 or FQKV_KV_FP8");
   if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32 && x_dtype != FQKV_SRC_BF16)
     return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16, FQKV_SRC_F32 or FQKV_SRC_BF16");
   if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
@@ -711,7 +711,7 @@ int fqkv_quantize_kv_append_at(const void* K_new, const void* V_new, int x_dtype
   if (!K_new || !V_new || !K_cache || !V_cache || !Ks_cache || !Vs_cache || !pos)
     return fail(FQKV_ERR_ARG, "null tensor pointer");
   const uintptr_t xal = (x_dtype != FQKV_SRC_F32 && D == 64) ? 8 : 16;
-  const uintptr_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
+  const uintptr_t qal = kv_format == FQKV_KV_I4 ? (D == 128 ? 4 : 2) : (D == 128 ? 8 : 4);
   if (!aligned(K_new, xal) || !aligned(V_new, xal)) return fail(FQKV_ERR_ARG, "K_new and V_new must be %d-byte aligned", (int)xal);
   if (!aligned(K_cache, qal) || !aligned(V_cache, qal)) return fail(FQKV_ERR_ARG, "caches must be %d-byte aligned", (int)qal);
   if (!aligned(Ks_cache, 2) || !aligned(Vs_cache, 2)) return fail(FQKV_ERR_ARG, "scales must be 2-byte aligned");
@@ -728,8 +728,8 @@ int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, co
                            void* Ks_pages, void* Vs_pages, int64_t num_pages, int64_t page_size,
                            int64_t page_stride, int64_t token_stride, int64_t head_stride, int64_t s_page_stride,
                            int64_t s_token_stride, int64_t s_head_stride, int kv_format, void* stream) {
-  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4)
-    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8 or FQKV_KV_I4");
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4 && kv_format != FQKV_KV_FP8)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8, FQKV_KV_I4 or FQKV_KV_FP8");
   if (x_dtype != FQKV_SRC_F16 && x_dtype != FQKV_SRC_F32 && x_dtype != FQKV_SRC_BF16)
     return fail(FQKV_ERR_ARG, "x_dtype must be FQKV_SRC_F16, FQKV_SRC_F32 or FQKV_SRC_BF16");
   if (D != 64 && D != 128) return fail(FQKV_ERR_ARG, "D: head_dim must be 64 or 128, got %lld", (long long)D);
@@ -740,7 +740,7 @@ int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, co
       num_pages > (INT64_MAX >> 31))
     return fail(FQKV_ERR_ARG, "page: num_pages must be in [1, 2^32) and page_size a power of two <= 2^30, got %lld "
                 "and %lld", (long long)num_pages, (long long)page_size);
-  const int64_t qal = kv_format == FQKV_KV_I8 ? (D == 128 ? 8 : 4) : (D == 128 ? 4 : 2);
+  const int64_t qal = kv_format == FQKV_KV_I4 ? (D == 128 ? 4 : 2) : (D == 128 ? 8 : 4);
   if (page_stride < 0 || token_stride < 0 || head_stride < 0 || page_stride % qal || token_stride % qal ||
       head_stride % qal)
     return fail(FQKV_ERR_ARG, "stride: code strides must be non-negative multiples of %lld bytes", (long long)qal);

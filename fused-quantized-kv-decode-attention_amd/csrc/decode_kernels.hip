@@ -659,7 +659,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // sum(q)) over the query as the operands carry it; qbias = BIAS sum(q) of
   // the lane's column (zero for fp16)
   float qbias = 0.0f;
-  if constexpr (F::QUANT) {
+  if constexpr (F::BIASED) {
     float qs = 0.0f;
 #pragma unroll
     for (int i = 0; i < F::NKI; ++i)
@@ -877,7 +877,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         const float raw = pick<P>(jm, [&](int j) { return c4[g * P + j][k]; });
-        x[g][k] = (F::QUANT ? fmaf(raw, 16777216.0f, -qbias) : raw) * (float)ks[g][k];
+        x[g][k] = (F::BIASED ? fmaf(raw, 16777216.0f, -qbias) : raw) * (float)ks[g][k];
       }
     if (!full) {
 #pragma unroll
@@ -938,7 +938,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
         const float pw = fast_exp2(fmaf(x[g][k], p.c, arg0));
         psum += pw;
         wv[k] = F::QUANT ? pw * (float)vs[g][k] : pw;
-        if constexpr (F::QUANT) wsum += wv[k];
+        if constexpr (F::BIASED) wsum += wv[k];
       }
       if constexpr (PVV) {
         if (live) {
@@ -976,7 +976,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     }
     const float acc_alpha = F::QUANT ? __builtin_amdgcn_ldexpf(alpha, shift - acc_shift) : alpha;
     l_run = l_run * acc_alpha + psum;
-    if constexpr (F::QUANT) w_run = w_run * acc_alpha + wsum;
+    if constexpr (F::BIASED) w_run = w_run * acc_alpha + wsum;
     acc_shift = shift;
     // acc needs rescaling only where the maximum or the shift moved and
     // something has been accumulated (acc is all zero while m = -inf)
@@ -1089,12 +1089,14 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // columns 0 .. HG - 1 hold every tile (fp16), or the P columns of a head
   // add up (int8 / int4) ----
   if constexpr (F::QUANT) {
-    // acc[c] * vunit = sum w (v + BIAS): take BIAS sum(w) of the column off
-    const float wb = F::BIAS * rows4_sum(w_run);
+    if constexpr (F::BIASED) {
+      // acc[c] * vunit = sum w (v + BIAS): take BIAS sum(w) of the column off
+      const float wb = F::BIAS * rows4_sum(w_run);
 #pragma unroll
-    for (int c = 0; c < VE; ++c)
+      for (int c = 0; c < VE; ++c)
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc[c][k] = fmaf(acc[c][k], F::vunit(c % VG::EPD), -wb);
+        for (int k = 0; k < 4; ++k) acc[c][k] = fmaf(acc[c][k], F::vunit(c % VG::EPD), -wb);
+    }
     l_run = __builtin_amdgcn_ldexpf(l_run, -acc_shift);
   }
   l_run = cols_sum<HG, P>(rows4_sum(l_run));
@@ -1303,7 +1305,7 @@ hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, i
     constexpr int HEAD_SPAN = 128;
     const int64_t nwsg = (int64_t)nblocks / p.S;
     const int d = p.split_major ? 8 : 8 / std::gcd(p.S, 8);
-    const int row_bytes = fmt == KV_I4 ? D / 2 : (fmt == KV_I8 ? D : 2 * D);
+    const int row_bytes = fmt == KV_I4 ? D / 2 : ((fmt == KV_I8 || fmt == KV_FP8) ? D : 2 * D);
     int k = 0;
     while ((2 << k) * row_bytes <= HEAD_SPAN && p.hkv % (2 << k) == 0 && p.kv_ts >= (2 << k) * row_bytes) ++k;
     int ld = 0;
@@ -1325,6 +1327,8 @@ hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, i
                                : launch_partial_d<KV_I4, 128>(hg, p, nblocks, nw, st);
     case KV_BF16: return D == 64 ? launch_partial_d<KV_BF16, 64>(hg, p, nblocks, nw, st)
                                  : launch_partial_d<KV_BF16, 128>(hg, p, nblocks, nw, st);
+    case KV_FP8: return D == 64 ? launch_partial_d<KV_FP8, 64>(hg, p, nblocks, nw, st)
+                                : launch_partial_d<KV_FP8, 128>(hg, p, nblocks, nw, st);
   }
   return hipErrorInvalidValue;
 }

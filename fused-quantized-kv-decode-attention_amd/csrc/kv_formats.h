@@ -50,7 +50,7 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
 
-enum KvFormat : int { KV_F16 = 0, KV_I8 = 1, KV_I4 = 2, KV_BF16 = 3 };
+enum KvFormat : int { KV_F16 = 0, KV_I8 = 1, KV_I4 = 2, KV_BF16 = 3, KV_FP8 = 4 };
 
 // v_perm_b32 byte selector: 0-3 pick bytes of the second operand, 4-7 of
 // the first, 0x0C gives a zero byte.
@@ -153,7 +153,8 @@ struct Fmt;
 // rows, which streamed ~6 % slower than whole rows on MI355X at batch 1.
 template <int D>
 struct Fmt<KV_F16, D> {
-  static constexpr bool QUANT = false;
+  static constexpr bool QUANT = false;   // per-token scales
+  static constexpr bool BIASED = false;  // operands carry x + BIAS in units (integer codes)
   static constexpr bool BF16 = false;  // operands are fp16 bit patterns
   static constexpr bool STAGE_K = true;
   // tile offsets in the loads' SGPR offset (instead of VGPR adds per load):
@@ -225,6 +226,7 @@ struct Fmt<KV_BF16, D> : Fmt<KV_F16, D> {
 template <int D>
 struct Fmt<KV_I8, D> {
   static constexpr bool QUANT = true;
+  static constexpr bool BIASED = true;
   static constexpr bool BF16 = false;
   static constexpr bool STAGE_K = false;
   static constexpr bool SOFF_TILE = false;
@@ -265,10 +267,45 @@ struct Fmt<KV_I8, D> {
   }
 };
 
+// ----------------------------------------------------------------- fp8 ----
+// OCP fp8 e4m3 codes (1 byte per element, as int8) with fp16 per-token
+// scales. gfx950 converts two codes to an fp16 pair in one instruction
+// (v_cvt_scalef32_pk_f16_fp8, scale 1), exactly: every e4m3 value is an fp16
+// value. So the operands are the true code values, with no bias and unit 1;
+// everything else (loads, scale handling, the weight shift) is int8's.
+__device__ __forceinline__ h2_t fp8x2_lo(uint32_t w) {
+  return __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false));
+}
+__device__ __forceinline__ h2_t fp8x2_hi(uint32_t w) {
+  return __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true));
+}
+
+template <int D>
+struct Fmt<KV_FP8, D> : Fmt<KV_I8, D> {
+  static constexpr bool BIASED = false;
+  static constexpr float BIAS = 0.0f;
+  __host__ __device__ static constexpr float kunit(int) { return 1.0f; }
+  __host__ __device__ static constexpr float vunit(int) { return 1.0f; }
+  __device__ static h8_t kfrag(const u4_t (&kr)[D / 64], int i) {
+    const u4_t v = kr[i / 2];
+    const uint32_t x = (i % 2) ? v.z : v.x, y = (i % 2) ? v.w : v.y;
+    const h2_t a = fp8x2_lo(x), b = fp8x2_hi(x), c = fp8x2_lo(y), d = fp8x2_hi(y);
+    return h8_t{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+  }
+  __device__ static uint32_t vprep(uint32_t x) { return x; }
+  // byte pos of dwords a and b -> half2 (a_pos, b_pos): the two codes into
+  // bytes 0 and 1, then one conversion
+  __device__ static h2_t vpair(uint32_t a, uint32_t b, int pos) {
+    const uint32_t sel = 0x0C0C0000u | ((uint32_t)(4 + pos) << 8) | (uint32_t)pos;
+    return fp8x2_lo(__builtin_amdgcn_perm(b, a, sel));
+  }
+};
+
 // ---------------------------------------------------------------- int4 ----
 template <int D>
 struct Fmt<KV_I4, D> {
   static constexpr bool QUANT = true;
+  static constexpr bool BIASED = true;
   static constexpr bool BF16 = false;
   static constexpr bool STAGE_K = false;
   static constexpr bool SOFF_TILE = true;

@@ -54,6 +54,8 @@ __device__ __forceinline__ float row16_max(float x) {
 // Source element types (the public header's FQKV_SRC_* values). bf16 rows
 // widen exactly to fp32 and then follow the fp32 expressions.
 enum { SRC_F16 = 0, SRC_F32 = 1, SRC_BF16 = 2 };
+// the largest fp8 e4m3 value; as QMAX it selects the fp8 codes
+constexpr int FP8_MAX = 448;
 
 template <int SRC, int EPL>
 __device__ __forceinline__ void load_row_slice(const void* X, int64_t row, int i, int D, float (&x)[EPL]) {
@@ -111,7 +113,11 @@ __device__ __forceinline__ void load_row_slice(const void* X, int64_t row, int i
 template <int SRC, int QMAX, int D>
 __device__ __forceinline__ void quantize_row(const void* __restrict__ X, int64_t row, uint8_t* __restrict__ qrow,
                                              _Float16* __restrict__ srow, bool live, int i) {
-  constexpr bool F16 = SRC == SRC_F16;  // fp16 rounding of the scale and the quotients
+  // QMAX 448: fp8 e4m3 codes (no counterpart in the reference), always the
+  // fp32 expressions: s = max(a * fp32(1/448), 1e-8), code = e4m3 round to
+  // nearest even of clamp(x / s, +-448), scale stored as fp16(s)
+  constexpr bool FP8 = QMAX == FP8_MAX;
+  constexpr bool F16 = SRC == SRC_F16 && !FP8;  // fp16 rounding of the scale and the quotients
   constexpr int EPL = D / 16;  // elements per lane
   float x[EPL];
   if (live) {
@@ -146,6 +152,7 @@ __device__ __forceinline__ void quantize_row(const void* __restrict__ X, int64_t
     return fmaf(fmaf(-q0, s, v), y, q0);
   };
   int q[EPL];
+  float qf[FP8 ? EPL : 1];
 #pragma unroll
   for (int e = 0; e < EPL; ++e) {
     float quot;
@@ -158,11 +165,30 @@ __device__ __forceinline__ void quantize_row(const void* __restrict__ X, int64_t
     } else {
       quot = divide(x[e]);
     }
-    const float r = fminf(fmaxf(__builtin_rintf(quot), -(float)QMAX), (float)QMAX);
-    q[e] = (int)r;
+    if constexpr (FP8) {
+      qf[e] = fminf(fmaxf(quot, -(float)FP8_MAX), (float)FP8_MAX);
+    } else {
+      const float r = fminf(fmaxf(__builtin_rintf(quot), -(float)QMAX), (float)QMAX);
+      q[e] = (int)r;
+    }
   }
   if (!live) return;
-  if constexpr (QMAX == 127) {
+  if constexpr (FP8) {
+    // v_cvt_pk_fp8_f32 rounds to nearest even (OCP e4m3; the clamp keeps it
+    // in range); two codes per call, into the low or the high half
+    uint32_t w[EPL / 4];
+#pragma unroll
+    for (int k = 0; k < EPL / 4; ++k) {
+      const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(qf[4 * k], qf[4 * k + 1], 0, false);
+      w[k] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(qf[4 * k + 2], qf[4 * k + 3], lo, true);
+    }
+    uint8_t* out = qrow + EPL * i;
+    if constexpr (EPL == 8) {
+      *(u2_t*)out = u2_t{w[0], w[1]};
+    } else {
+      *(uint32_t*)out = w[0];
+    }
+  } else if constexpr (QMAX == 127) {
     uint32_t w[EPL / 4];
 #pragma unroll
     for (int k = 0; k < EPL / 4; ++k)
@@ -192,7 +218,7 @@ __device__ __forceinline__ void quantize_row(const void* __restrict__ X, int64_t
 // Destination row dst of a contiguous [rows, D or D/2] code buffer.
 template <int QMAX, int D>
 __device__ __forceinline__ uint8_t* code_row(uint8_t* Q, int64_t dst) {
-  return Q + dst * (QMAX == 127 ? D : D / 2);
+  return Q + dst * (QMAX == 7 ? D / 2 : D);
 }
 
 template <int SRC, int QMAX, int D>
@@ -326,6 +352,7 @@ hipError_t by_src_fmt(int src, int fmt, Fn f) {
   auto q = [&](auto src_c) -> hipError_t {
     if (fmt == KV_I8) return f(src_c, std::integral_constant<int, 127>());
     if (fmt == KV_I4) return f(src_c, std::integral_constant<int, 7>());
+    if (fmt == KV_FP8) return f(src_c, std::integral_constant<int, FP8_MAX>());
     return hipErrorInvalidValue;
   };
   switch (src) {

@@ -50,6 +50,16 @@ void check_W(int64_t W) { TORCH_CHECK(W == 2 || W == 4 || W == 8, "W: must be 2,
 
 void check_D(int64_t D) { TORCH_CHECK(D == 64 || D == 128, "D: head_dim must be 64 or 128, got ", D); }
 
+// KV code format of a quantized cache tensor's dtype (FQKV_KV_I8 / _I4 / _FP8), -1 for any other.
+int code_format(const torch::Tensor& C) {
+  switch (C.scalar_type()) {
+    case torch::kChar: return FQKV_KV_I8;
+    case torch::kByte: return FQKV_KV_I4;
+    case torch::kFloat8_e4m3fn: return FQKV_KV_FP8;
+    default: return -1;
+  }
+}
+
 // Quantizer source element type (FQKV_SRC_*), -1 for any other dtype.
 int src_of(const torch::Tensor& X) {
   switch (X.scalar_type()) {
@@ -104,7 +114,7 @@ torch::Tensor quant_common(int fmt, torch::Tensor q, torch::Tensor K, torch::Ten
                 "packed uint8: K and V must be uint8 holding two int4 values per byte");
   }
   TORCH_CHECK(q.dim() == 2 && K.dim() == 3 && V.sizes() == K.sizes() && q.size(0) == K.size(0),
-              "shape: expected q [B,D], K and V [B,N,", fmt == FQKV_KV_I8 ? "D" : "D/2", "]; got q ", q.sizes(),
+              "shape: expected q [B,D], K and V [B,N,", fmt == FQKV_KV_I4 ? "D/2" : "D", "]; got q ", q.sizes(),
               ", K ", K.sizes(), ", V ", V.sizes());
   const int64_t B = K.size(0), N = K.size(1);
   const int64_t D = fmt == FQKV_KV_I8 ? K.size(2) : 2 * K.size(2);
@@ -226,13 +236,16 @@ void gqa_sk_fast_timed(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch:
 int64_t quant_kv_dims(int fmt, const torch::Tensor& K, const torch::Tensor& V) {
   if (fmt == FQKV_KV_I8) {
     TORCH_CHECK(K.scalar_type() == torch::kChar && V.scalar_type() == torch::kChar, "int8: K and V must be int8");
+  } else if (fmt == FQKV_KV_FP8) {
+    TORCH_CHECK(K.scalar_type() == torch::kFloat8_e4m3fn && V.scalar_type() == torch::kFloat8_e4m3fn,
+                "fp8: K and V must be float8_e4m3fn");
   } else {
     TORCH_CHECK(K.scalar_type() == torch::kByte && V.scalar_type() == torch::kByte,
                 "packed uint8: K and V must be uint8 holding two int4 values per byte");
   }
   TORCH_CHECK(V.sizes() == K.sizes(), "shape: K and V must have the same shape; got ", K.sizes(), " and ",
               V.sizes());
-  const int64_t D = fmt == FQKV_KV_I8 ? K.size(-1) : 2 * K.size(-1);
+  const int64_t D = fmt == FQKV_KV_I4 ? 2 * K.size(-1) : K.size(-1);
   check_D(D);
   return D;
 }
@@ -245,7 +258,7 @@ torch::Tensor decode_attn_gqa_quant(int fmt, torch::Tensor q, torch::Tensor K, t
   check_half(Ks, "Ks");
   check_half(Vs, "Vs");
   TORCH_CHECK(q.dim() == 3 && K.dim() == 4 && q.size(0) == K.size(0),
-              "shape: expected q [B,Hq,D], K and V [B,Hkv,N,", fmt == FQKV_KV_I8 ? "D" : "D/2", "]; got q ",
+              "shape: expected q [B,Hq,D], K and V [B,Hkv,N,", fmt == FQKV_KV_I4 ? "D/2" : "D", "]; got q ",
               q.sizes(), ", K ", K.sizes());
   const int64_t D = quant_kv_dims(fmt, K, V);
   const int64_t B = q.size(0), Hq = q.size(1), Hkv = K.size(1), N = K.size(2);
@@ -274,6 +287,10 @@ torch::Tensor decode_attn_gqa_int4(torch::Tensor q, torch::Tensor K, torch::Tens
                                    torch::Tensor Vs, int64_t W) {
   return decode_attn_gqa_quant(FQKV_KV_I4, q, K, V, Ks, Vs, W);
 }
+torch::Tensor decode_attn_gqa_fp8(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks,
+                                  torch::Tensor Vs, int64_t W) {
+  return decode_attn_gqa_quant(FQKV_KV_FP8, q, K, V, Ks, Vs, W);
+}
 
 // gqa_sk_fast_int8 / _int4 (q[Hq,D], K[Hkv,N,D or D/2], V, Ks[Hkv,N], Vs, m_part, l_part, o_part, o, S, W, CW)
 void gqa_sk_fast_quant(int fmt, torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks,
@@ -288,7 +305,7 @@ void gqa_sk_fast_quant(int fmt, torch::Tensor q, torch::Tensor K, torch::Tensor 
                   o_part.scalar_type() == torch::kFloat,
               "partial: m_part, l_part and o_part must be float32");
   TORCH_CHECK(q.dim() == 2 && K.dim() == 3, "shape: expected q [Hq,D], K and V [Hkv,N,",
-              fmt == FQKV_KV_I8 ? "D" : "D/2", "]; got q ", q.sizes(), ", K ", K.sizes());
+              fmt == FQKV_KV_I4 ? "D/2" : "D", "]; got q ", q.sizes(), ", K ", K.sizes());
   const int64_t D = quant_kv_dims(fmt, K, V);
   const int64_t Hq = q.size(0), Hkv = K.size(0), N = K.size(1);
   TORCH_CHECK(q.size(1) == D, "shape: q head_dim ", q.size(1), " does not match KV head_dim ", D);
@@ -320,11 +337,16 @@ void gqa_sk_fast_int4(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::
                       int64_t W, int64_t CW) {
   gqa_sk_fast_quant(FQKV_KV_I4, q, K, V, Ks, Vs, m_part, l_part, o_part, o, S, W, CW);
 }
+void gqa_sk_fast_fp8(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor Ks, torch::Tensor Vs,
+                     torch::Tensor m_part, torch::Tensor l_part, torch::Tensor o_part, torch::Tensor o, int64_t S,
+                     int64_t W, int64_t CW) {
+  gqa_sk_fast_quant(FQKV_KV_FP8, q, K, V, Ks, Vs, m_part, l_part, o_part, o, S, W, CW);
+}
 
 // ---- other KV layouts (no counterpart in the reference) ----
 
 // int8 / int4 codes, which come with per-token scales
-bool quant_fmt(int fmt) { return fmt == FQKV_KV_I8 || fmt == FQKV_KV_I4; }
+bool quant_fmt(int fmt) { return fmt == FQKV_KV_I8 || fmt == FQKV_KV_I4 || fmt == FQKV_KV_FP8; }
 
 // KV format from K's dtype; returns FQKV_KV_*, sets D (unpacked head_dim) and the element size.
 int kv_format_of(const torch::Tensor& K, int64_t* D, int64_t* elem) {
@@ -333,10 +355,10 @@ int kv_format_of(const torch::Tensor& K, int64_t* D, int64_t* elem) {
     *elem = 2;
     return K.scalar_type() == torch::kHalf ? FQKV_KV_F16 : FQKV_KV_BF16;
   }
-  if (K.scalar_type() == torch::kChar) {
+  if (K.scalar_type() == torch::kChar || K.scalar_type() == torch::kFloat8_e4m3fn) {
     *D = K.size(-1);
     *elem = 1;
-    return FQKV_KV_I8;
+    return K.scalar_type() == torch::kChar ? FQKV_KV_I8 : FQKV_KV_FP8;
   }
   TORCH_CHECK(K.scalar_type() == torch::kByte, "fp16: K must be float16, bfloat16, int8 or packed uint8 (int4)");
   *D = 2 * K.size(-1);
@@ -527,7 +549,9 @@ static std::vector<torch::Tensor> quantize_per_token(torch::Tensor X, int fmt) {
   const c10::DeviceGuard guard(X.device());
   auto qsizes = X.sizes().vec();
   if (fmt == FQKV_KV_I4) qsizes.back() = D / 2;
-  auto Q = torch::empty(qsizes, X.options().dtype(fmt == FQKV_KV_I8 ? torch::kChar : torch::kByte));
+  auto Q = torch::empty(qsizes, X.options().dtype(fmt == FQKV_KV_I8   ? torch::kChar
+                                                  : fmt == FQKV_KV_FP8 ? torch::kFloat8_e4m3fn
+                                                                       : torch::kByte));
   auto ssizes = X.sizes().vec();
   ssizes.pop_back();
   auto S = torch::empty(ssizes, X.options().dtype(torch::kHalf));
@@ -543,6 +567,9 @@ static std::vector<torch::Tensor> quantize_int8_per_token(torch::Tensor X) {
 static std::vector<torch::Tensor> quantize_int4_per_token(torch::Tensor X) {
   return quantize_per_token(X, FQKV_KV_I4);
 }
+static std::vector<torch::Tensor> quantize_fp8_per_token(torch::Tensor X) {
+  return quantize_per_token(X, FQKV_KV_FP8);
+}
 
 // quantize_kv_append_(K_new[B,H,n,D], V_new, K_cache[B,H,cap,D or D/2], V_cache, Ks_cache[B,H,cap],
 // Vs_cache, pos) -> None: quantizes the new tokens into cache positions pos .. pos+n-1 in place.
@@ -553,14 +580,13 @@ static void quantize_kv_append(torch::Tensor Kn, torch::Tensor Vn, torch::Tensor
               "fp16: K_new must be float16, float32 or bfloat16");
   TORCH_CHECK(Vn.scalar_type() == Kn.scalar_type() && Vn.sizes() == Kn.sizes() && Kn.dim() == 4,
               "shape: K_new and V_new must be [B,H,n,D] of one dtype; got ", Kn.sizes(), " and ", Vn.sizes());
-  TORCH_CHECK(Kc.scalar_type() == torch::kChar || Kc.scalar_type() == torch::kByte,
-              "int8: caches must be int8 or packed uint8 (int4)");
-  const int fmt = Kc.scalar_type() == torch::kChar ? FQKV_KV_I8 : FQKV_KV_I4;
+  const int fmt = code_format(Kc);
+  TORCH_CHECK(fmt >= 0, "int8: caches must be int8, packed uint8 (int4) or float8_e4m3fn");
   const int64_t B = Kn.size(0), H = Kn.size(1), n = Kn.size(2), D = Kn.size(3);
   check_D(D);
-  TORCH_CHECK(Kc.dim() == 4 && Kc.size(0) == B && Kc.size(1) == H && Kc.size(3) == (fmt == FQKV_KV_I8 ? D : D / 2) &&
+  TORCH_CHECK(Kc.dim() == 4 && Kc.size(0) == B && Kc.size(1) == H && Kc.size(3) == (fmt == FQKV_KV_I4 ? D / 2 : D) &&
                   Vc.sizes() == Kc.sizes() && Vc.scalar_type() == Kc.scalar_type(),
-              "shape: caches must be [B,H,capacity,", fmt == FQKV_KV_I8 ? "D" : "D/2", "] matching K_new ", Kn.sizes(),
+              "shape: caches must be [B,H,capacity,", fmt == FQKV_KV_I4 ? "D/2" : "D", "] matching K_new ", Kn.sizes(),
               "; got ", Kc.sizes(), " and ", Vc.sizes());
   const int64_t cap = Kc.size(2);
   check_half(Ksc, "Ks_cache");
@@ -586,14 +612,13 @@ static void quantize_kv_append_at(torch::Tensor Kn, torch::Tensor Vn, torch::Ten
               "fp16: K_new must be float16, float32 or bfloat16");
   TORCH_CHECK(Vn.scalar_type() == Kn.scalar_type() && Vn.sizes() == Kn.sizes() && Kn.dim() == 4,
               "shape: K_new and V_new must be [B,H,n,D] of one dtype; got ", Kn.sizes(), " and ", Vn.sizes());
-  TORCH_CHECK(Kc.scalar_type() == torch::kChar || Kc.scalar_type() == torch::kByte,
-              "int8: caches must be int8 or packed uint8 (int4)");
-  const int fmt = Kc.scalar_type() == torch::kChar ? FQKV_KV_I8 : FQKV_KV_I4;
+  const int fmt = code_format(Kc);
+  TORCH_CHECK(fmt >= 0, "int8: caches must be int8, packed uint8 (int4) or float8_e4m3fn");
   const int64_t B = Kn.size(0), H = Kn.size(1), n = Kn.size(2), D = Kn.size(3);
   check_D(D);
-  TORCH_CHECK(Kc.dim() == 4 && Kc.size(0) == B && Kc.size(1) == H && Kc.size(3) == (fmt == FQKV_KV_I8 ? D : D / 2) &&
+  TORCH_CHECK(Kc.dim() == 4 && Kc.size(0) == B && Kc.size(1) == H && Kc.size(3) == (fmt == FQKV_KV_I4 ? D / 2 : D) &&
                   Vc.sizes() == Kc.sizes() && Vc.scalar_type() == Kc.scalar_type(),
-              "shape: caches must be [B,H,capacity,", fmt == FQKV_KV_I8 ? "D" : "D/2", "] matching K_new ", Kn.sizes(),
+              "shape: caches must be [B,H,capacity,", fmt == FQKV_KV_I4 ? "D/2" : "D", "] matching K_new ", Kn.sizes(),
               "; got ", Kc.sizes(), " and ", Vc.sizes());
   const int64_t cap = Kc.size(2);
   check_half(Ksc, "Ks_cache");
@@ -624,14 +649,13 @@ static void quantize_kv_to_pages(torch::Tensor Kn, torch::Tensor Vn, torch::Tens
               "fp16: K_new must be float16, float32 or bfloat16");
   TORCH_CHECK(Kn.dim() == 3 && Vn.sizes() == Kn.sizes() && Vn.scalar_type() == Kn.scalar_type(),
               "shape: K_new and V_new must be [T,Hkv,D] of one dtype; got ", Kn.sizes(), " and ", Vn.sizes());
-  TORCH_CHECK(Kp.scalar_type() == torch::kChar || Kp.scalar_type() == torch::kByte,
-              "int8: pages must be int8 or packed uint8 (int4)");
-  const int fmt = Kp.scalar_type() == torch::kChar ? FQKV_KV_I8 : FQKV_KV_I4;
+  const int fmt = code_format(Kp);
+  TORCH_CHECK(fmt >= 0, "int8: pages must be int8, packed uint8 (int4) or float8_e4m3fn");
   const int64_t T = Kn.size(0), H = Kn.size(1), D = Kn.size(2);
   check_D(D);
-  TORCH_CHECK(Kp.dim() == 4 && Kp.size(2) == H && Kp.size(3) == (fmt == FQKV_KV_I8 ? D : D / 2) &&
+  TORCH_CHECK(Kp.dim() == 4 && Kp.size(2) == H && Kp.size(3) == (fmt == FQKV_KV_I4 ? D / 2 : D) &&
                   Vp.sizes() == Kp.sizes() && Vp.strides() == Kp.strides() && Vp.scalar_type() == Kp.scalar_type(),
-              "shape: pages must be [P,page_size,", H, ",", fmt == FQKV_KV_I8 ? "D" : "D/2",
+              "shape: pages must be [P,page_size,", H, ",", fmt == FQKV_KV_I4 ? "D/2" : "D",
               "] with equal strides; got ", Kp.sizes(), " and ", Vp.sizes());
   TORCH_CHECK(Kp.stride(3) == 1, "contig: the last dim of the pages must be contiguous");
   check_half(Ksp, "Ks_pages");
@@ -684,6 +708,11 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gqa_sk_fast_int4", &gqa_sk_fast_int4, "GQA split-K int4-KV decode", py::arg("q"), py::arg("K"),
         py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("m_part"), py::arg("l_part"), py::arg("o_part"),
         py::arg("o"), py::arg("S"), py::arg("W"), py::arg("CW"));
+  m.def("decode_attn_gqa_fp8", &decode_attn_gqa_fp8, "GQA-aware fp8 (e4m3) KV decode", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("W"));
+  m.def("gqa_sk_fast_fp8", &gqa_sk_fast_fp8, "GQA split-K fp8 (e4m3) KV decode", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("m_part"), py::arg("l_part"), py::arg("o_part"),
+        py::arg("o"), py::arg("S"), py::arg("W"), py::arg("CW"));
   m.def("decode_attn_gqa_nhd", &decode_attn_gqa_nhd, "GQA decode over a token-major [B,N,Hkv,D] KV cache",
         py::arg("q"), py::arg("K"), py::arg("V"), py::arg("W"), py::arg("Ks") = py::none(),
         py::arg("Vs") = py::none());
@@ -697,6 +726,8 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "per-token int8 KV quantizer on the GPU -> (int8 [..., D], fp16 scales [...])", py::arg("X"));
   m.def("quantize_int4_per_token", &quantize_int4_per_token,
         "per-token int4 KV quantizer on the GPU -> (packed uint8 [..., D/2], fp16 scales [...])", py::arg("X"));
+  m.def("quantize_fp8_per_token", &quantize_fp8_per_token,
+        "per-token fp8 e4m3 KV quantizer on the GPU -> (float8_e4m3fn [..., D], fp16 scales [...])", py::arg("X"));
   m.def("quantize_kv_append_", &quantize_kv_append,
         "quantize new K/V tokens [B,H,n,D] into int8 / int4 caches [B,H,capacity,.] at position pos, in place",
         py::arg("K_new"), py::arg("V_new"), py::arg("K_cache"), py::arg("V_cache"), py::arg("Ks_cache"),

@@ -18,6 +18,9 @@ Beyond the reference (same conventions, no counterpart there):
         m_part, l_part, o_part, o, S, W, CW)        split-K over an int8 / int4 cache
     quantize_int8_per_token / quantize_int4_per_token(X[..., D]) -> (bytes, fp16 scales)
                                                     the KV quantizers as GPU kernels
+    decode_attn_gqa_fp8 / gqa_sk_fast_fp8 / quantize_fp8_per_token
+                                                    the same over OCP fp8 e4m3 codes
+                                                    (float8_e4m3fn) with fp16 per-token scales
     quantize_kv_append_(K_new[B,H,n,D], V_new, K_cache[B,H,cap,D or D/2], V_cache,
         Ks_cache[B,H,cap], Vs_cache, pos) -> None  the quantizers in append form for a live
                                                     cache: one launch, in place at pos
@@ -65,6 +68,9 @@ __all__ = [
     "gqa_sk_fast_int4",
     "quantize_int8_per_token",
     "quantize_int4_per_token",
+    "decode_attn_gqa_fp8",
+    "gqa_sk_fast_fp8",
+    "quantize_fp8_per_token",
     "quantize_kv_append_",
     "quantize_kv_append_at_",
     "quantize_kv_to_pages_",
@@ -78,7 +84,8 @@ __all__ = [
 
 _ENTRY_POINTS = ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa",
                  "gqa_sk_fast", "decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8",
-                 "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token", "quantize_kv_append_",
+                 "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token", "decode_attn_gqa_fp8",
+                 "gqa_sk_fast_fp8", "quantize_fp8_per_token", "quantize_kv_append_",
                  "quantize_kv_append_at_", "quantize_kv_to_pages_", "decode_attn_gqa_nhd", "decode_attn_gqa_strided", "decode_attn_gqa_paged")
 _EXT = None
 

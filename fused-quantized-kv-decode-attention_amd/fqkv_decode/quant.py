@@ -65,3 +65,28 @@ def dequant_int8(q, s):
 def dequant_int4(packed, s):
     """Unpack (low nibble first), then (float)q * (float)scale -> fp32 [..., N, D]."""
     return unpack_int4(packed).float() * s.float()[..., None]
+
+
+def quant_fp8_per_token(X):
+    """X [..., N, D] (fp16, bf16 or fp32) -> (float8_e4m3fn [..., N, D], fp16 scales [..., N]).
+
+    The fp8 KV format (no counterpart in the reference): in fp32 on the widened
+    input, s = max(max|x| * fp32(1/448), 1e-8) and code = e4m3(clamp(x / s, +-448))
+    rounded to nearest even, an exact zero stored as +0; the scale is stored as fp16(s).
+    """
+    X32 = X.float()
+    a = X32.abs().amax(-1, keepdim=True)
+    s = (a * _recip32(448.0)).clamp(min=1e-8)
+    q = (X32 / s).clamp(-448.0, 448.0)
+    q = torch.where(q == 0, torch.zeros_like(q), q)
+    return q.to(torch.float8_e4m3fn).contiguous(), s.squeeze(-1).half().contiguous()
+
+
+def _recip32(x):
+    """fp32(1/x) as a 0-dim fp32 tensor (the multiplier the kernels use)."""
+    return torch.tensor(1.0, dtype=torch.float32) / torch.tensor(x, dtype=torch.float32)
+
+
+def dequant_fp8(q, s):
+    """float(code) * float(scale) -> fp32 [..., N, D]."""
+    return q.float() * s.float()[..., None]

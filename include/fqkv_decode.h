@@ -54,10 +54,12 @@ enum {
 };
 
 /* KV element formats: fp16 (the reference's), int8 and packed int4 codes with
- * fp16 per-token scales (the reference's quantized formats), and bf16 (no
- * counterpart in the reference; accepted by the strided and paged entry
- * points, for caches kept in a bf16 model's own dtype). */
-enum { FQKV_KV_F16 = 0, FQKV_KV_I8 = 1, FQKV_KV_I4 = 2, FQKV_KV_BF16 = 3 };
+ * fp16 per-token scales (the reference's quantized formats), bf16 (accepted by
+ * the strided and paged entry points, for caches kept in a bf16 model's own
+ * dtype) and OCP fp8 e4m3 codes with fp16 per-token scales (accepted wherever
+ * int8 is; value = code * scale). bf16 and fp8 have no counterpart in the
+ * reference. */
+enum { FQKV_KV_F16 = 0, FQKV_KV_I8 = 1, FQKV_KV_I4 = 2, FQKV_KV_BF16 = 3, FQKV_KV_FP8 = 4 };
 
 /* element type of a quantizer input; bf16 rows widen exactly to fp32 and are
  * quantized as fp32 (no counterpart in the reference, whose quantizers see

@@ -16,12 +16,15 @@ The oracle restates, in numpy, what the reference computes:
 * ``quant_int8_per_token`` -- tests/test_kernels.py:32-34 and nb:236-238
 * ``quant_int4_per_token`` / ``dequant_int4`` -- nb:292-307
 * ``dequant_int8``     -- decode_attn_int8_mw.cu:22-31 (float(q) * float(scale))
+* ``quant_fp8_per_token`` / ``dequant_fp8`` / ``e4m3_*`` -- no counterpart in the
+  reference: this library's fp8 e4m3 KV format, stated here as its definition
 
 Every function is pinned in ``tests/test_oracle.py`` by a check that a
 plausible mistake would fail: the reference notebook's recorded CPU-RNG int4
 figure (nb:283, rel 7.1036e-02), hand-built known-answer bytes, closed forms
 (N=1, q=0, a dominant key), the PyTorch library routines
-(``scaled_dot_product_attention`` and half/float tensor arithmetic), and
+(``scaled_dot_product_attention``, half/float tensor arithmetic and the float8_e4m3fn
+conversions), and
 brute-force loops on tiny inputs. No function here is "parity unpinned".
 """
 
@@ -41,4 +44,8 @@ from .quant import (  # noqa: F401
     dequant_int4,
     pack_int4,
     unpack_int4,
+    e4m3_encode,
+    e4m3_decode,
+    quant_fp8_per_token,
+    dequant_fp8,
 )

@@ -124,3 +124,61 @@ def dequant_int4(P, Ks):
     decode_attn_int4.cu:21-23,29-31; nb:301-307.
     """
     return unpack_int4(P).astype(np.float32) * np.asarray(Ks).astype(np.float32)[..., None]
+
+
+# ------------------------------------------------------------------ fp8 ----
+# OCP fp8 e4m3 ("E4M3FN"): 1 sign bit, 4 exponent bits (bias 7), 3 mantissa
+# bits, no infinities; S.1111.111 is NaN; the largest finite value is 448, the
+# smallest normal 2^-6, the subnormal step 2^-9. The fp8 KV format has no
+# counterpart in the reference: it is this library's own, defined here as the
+# fp32 expressions below (the same shape as the int8 quantizer, with the
+# round-to-nearest-even of e4m3 in place of round-to-integer).
+
+FP8_MAX = 448.0
+
+
+def e4m3_encode(x):
+    """float32 values with |x| <= 448 -> e4m3 codes (uint8), round to nearest even."""
+    x = np.asarray(x, dtype=np.float32)
+    sign = np.signbit(x).astype(np.uint16) << 7
+    a = np.abs(x).astype(np.float64)
+    _, e = np.frexp(a)
+    e = np.maximum(e - 1, -6)                 # binade of a (subnormals share 2^-6)
+    step = np.ldexp(1.0, e - 3)               # 3 mantissa bits
+    q = np.rint(a / step) * step              # exact in float64; may carry to 2^(e+1)
+    _, e2 = np.frexp(q)
+    e2 = e2 - 1
+    normal = q >= 2.0 ** -6
+    exp_field = np.where(normal, e2 + 7, 0).astype(np.uint16)
+    mant = np.where(normal, np.rint((q / np.ldexp(1.0, e2) - 1.0) * 8.0), np.rint(q / 2.0 ** -9)).astype(np.uint16)
+    return (sign | (exp_field << 3) | mant).astype(np.uint8)
+
+
+def e4m3_decode(codes):
+    """e4m3 codes (uint8) -> float32 values (NaN for S.1111.111)."""
+    c = np.asarray(codes, dtype=np.uint8).astype(np.int32)
+    e = (c >> 3) & 0xF
+    m = c & 0x7
+    mag = np.where(e == 0, m * 2.0 ** -9, (1.0 + m / 8.0) * np.ldexp(1.0, e - 7))
+    val = np.where((c & 0x80) != 0, -mag, mag)
+    return np.where((c & 0x7F) == 0x7F, np.nan, val).astype(np.float32)
+
+
+def quant_fp8_per_token(X):
+    """Per-token fp8 e4m3: returns (uint8 codes [..., D], fp16 scales [...]).
+
+    In fp32 on the widened input (fp16 and bf16 widen exactly): a = max|x|,
+    s = max(a * fp32(1/448), 1e-8), code = e4m3(clamp(x / s, -448, 448)) with
+    a true fp32 division (an exact zero as +0); the stored scale is fp16(s).
+    """
+    X32 = np.asarray(X).astype(np.float32)
+    a = np.abs(X32).max(axis=-1, keepdims=True)
+    s = np.maximum(a * _recip(FP8_MAX), np.float32(1e-8)).astype(np.float32)
+    q = np.clip(X32 / s, np.float32(-FP8_MAX), np.float32(FP8_MAX))
+    q = np.where(q == 0, np.float32(0.0), q)  # an exact zero (x = -0 too) is stored as +0
+    return e4m3_encode(q), s[..., 0].astype(np.float16)
+
+
+def dequant_fp8(codes, Ks):
+    """e4m3 value of each code times float(scale), in fp32 (exact: 4 x 11 significant bits)."""
+    return e4m3_decode(codes) * np.asarray(Ks).astype(np.float32)[..., None]

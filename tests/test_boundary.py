@@ -243,7 +243,7 @@ def test_capi_layout_entry_points_reject_bad_args(lib):
     # bf16 (kv_format 3) is a layout format: accepted, so the next check speaks (token stride < 256 B)
     assert fs(*[16] * 6, 1, 32, 8, 64, 128, 3, 65536, 256, 128, 0, 0, 1, 8, None, 0, None) == 1
     assert _err(lib).startswith("strides:") and "256" in _err(lib)
-    assert fs(*[16] * 6, 1, 32, 8, 64, 128, 4, 65536, 256, 256, 0, 0, 1, 8, None, 0, None) == 1
+    assert fs(*[16] * 6, 1, 32, 8, 64, 128, 5, 65536, 256, 256, 0, 0, 1, 8, None, 0, None) == 1
     assert "kv_format" in _err(lib)
 
 

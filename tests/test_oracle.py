@@ -306,3 +306,85 @@ def test_dequant_is_exact_fp32_product(bits):
 def test_round_fp16_is_nearest_even():
     x = np.array([1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, 65519.0, -0.0])
     np.testing.assert_array_equal(oracle.round_fp16(x).astype(np.float64), [1.0, 1.0 + 2 * 2.0 ** -10, 65504.0, -0.0])
+
+
+# ------------------------------------------------------------------ fp8 ----
+# The fp8 e4m3 KV format has no counterpart in the reference; the oracle states
+# its definition, pinned here against torch's float8_e4m3fn conversions (a
+# library routine), a brute-force grid and known answers.
+
+def test_e4m3_decode_matches_torch_for_every_code():
+    import torch
+
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = oracle.e4m3_decode(codes)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.isnan(got).sum() == 2  # 0x7F, 0xFF
+    np.testing.assert_array_equal(got[~np.isnan(got)], ref[~np.isnan(ref)])
+    assert got[0x7E] == 448.0 and got[0x08] == 2.0 ** -6 and got[0x01] == 2.0 ** -9 and got[0xB8] == -1.0
+
+
+def test_e4m3_encode_is_round_to_nearest_even():
+    """Against torch on every representable value, every midpoint between neighbours (ties: to
+    the even code), the floats next to each midpoint, subnormals and random values; and against
+    a brute-force nearest search on a grid."""
+    import torch
+
+    vals = np.unique(oracle.e4m3_decode(np.arange(256, dtype=np.uint8)))
+    vals = vals[~np.isnan(vals)]
+    mids = ((vals[:-1].astype(np.float64) + vals[1:]) / 2).astype(np.float32)
+    x = np.concatenate([vals, mids, np.nextafter(mids, np.float32(-1000)), np.nextafter(mids, np.float32(1000)),
+                        (_rng(30).standard_normal(100000) * 60).astype(np.float32),
+                        np.float32([2.0 ** -10, 3 * 2.0 ** -11, 1e-30, -1e-30])])
+    x = x[np.abs(x) <= 448]
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(oracle.e4m3_encode(x), ref)
+    # brute force: the nearest representable value, ties to the even mantissa
+    grid = np.linspace(-448, 448, 20001).astype(np.float32)
+    finite = np.arange(256, dtype=np.uint8)[~np.isnan(oracle.e4m3_decode(np.arange(256, dtype=np.uint8)))]
+    fv = oracle.e4m3_decode(finite).astype(np.float64)
+    for xv in grid[::37]:
+        d = np.abs(fv - float(xv))
+        best = finite[d == d.min()]
+        code = oracle.e4m3_encode(np.float32([xv]))[0]
+        assert code in best and (len(best) == 1 or (code & 1) == 0 or oracle.e4m3_decode(np.uint8([code]))[0] == 0)
+
+
+def test_fp8_quantizer_known_answers_and_invariants():
+    X = np.zeros((3, 8), np.float32)
+    X[0, :4] = [448.0, -224.0, 1.0, 0.0]   # s = 448 * fp32(1/448), codes near the values
+    X[1, :] = 0.0                           # all zero: s = 1e-8, codes 0
+    X[2, :3] = [1e-3, -2e-3, -0.0]
+    q, s = oracle.quant_fp8_per_token(X)
+    assert s.dtype == np.float16 and q.dtype == np.uint8
+    s32 = np.float32(448.0) * (np.float32(1.0) / np.float32(448.0))
+    assert s[0] == np.float16(s32)
+    np.testing.assert_array_equal(oracle.e4m3_decode(q[0, :4]), np.float32([448.0, -224.0, 1.0, 0.0]))
+    assert not q[1].any() and s[1] == np.float16(1e-8)
+    assert q[2, 2] == 0  # -0 is stored as +0
+    # every code decodes within half a step of x / s; the row maximum maps to +-448
+    Y = _rng(31).standard_normal((50, 128)).astype(np.float32) * 7
+    q, s = oracle.quant_fp8_per_token(Y)
+    s32 = np.maximum(np.abs(Y).max(-1) * (np.float32(1.0) / np.float32(448.0)), np.float32(1e-8))
+    r = Y / s32[:, None]
+    v = oracle.e4m3_decode(q)
+    assert np.all(np.abs(v - r) <= np.abs(r) * 2.0 ** -4 + 2.0 ** -10)
+    assert np.all(np.abs(v).max(-1) == 448.0)
+
+
+def test_fp8_quantizer_matches_the_pytorch_restatement():
+    """fqkv_decode.quant.quant_fp8_per_token (torch tensor ops, float8_e4m3fn conversion) gives the
+    oracle's bytes for fp32, fp16 and bf16 rows."""
+    import torch
+    from fqkv_decode import quant
+
+    g = torch.Generator().manual_seed(32)
+    for dt in (torch.float32, torch.float16, torch.bfloat16):
+        X = (torch.randn(16, 33, 128, generator=g) * 3).to(dt)
+        X[0, 0] = 0
+        X[0, 1, :5] = -0.0
+        q, s = quant.quant_fp8_per_token(X)
+        oq, os_ = oracle.quant_fp8_per_token(X.float().numpy())
+        np.testing.assert_array_equal(q.view(torch.uint8).numpy(), oq)
+        np.testing.assert_array_equal(s.numpy(), os_)
+        np.testing.assert_array_equal(quant.dequant_fp8(q, s).numpy(), oracle.dequant_fp8(oq, os_))
