@@ -401,7 +401,9 @@ REF_QUANT_D64_MS = {8: (0.2263, 0.2478, 0.2662), 256: (0.4792, 0.4864, 0.4915), 
 
 def suite_mha_quant(torch, fq, steps, warmup, rows, shapes=None):
     """fp16 / int8 / int4 MHA decode at B in {8, 256, 2048}, N=4096, W=8, at D=128 and at the
-    reference's own D=64 (its A100 numbers alongside); shapes: (D, B) pairs to run instead."""
+    reference's own D=64 (its A100 numbers alongside); fp8 (no counterpart in the reference)
+    through decode_attn_gqa_fp8 with one query head per KV head; shapes: (D, B) pairs to run
+    instead."""
     from fqkv_decode import quant
     N, W = 4096, 8
     if shapes is None:
@@ -409,8 +411,9 @@ def suite_mha_quant(torch, fq, steps, warmup, rows, shapes=None):
     for Dm, B in shapes:
         g = torch.Generator(device="cuda").manual_seed(1)
         q = torch.randn(B, Dm, device="cuda", generator=g).half()
-        per = {"fp16": 2 * B * N * Dm * 2, "int8": 2 * B * N * Dm + 4 * B * N, "int4": B * N * Dm + 4 * B * N}
-        for fmt in ("fp16", "int8", "int4"):
+        per = {"fp16": 2 * B * N * Dm * 2, "int8": 2 * B * N * Dm + 4 * B * N, "int4": B * N * Dm + 4 * B * N,
+               "fp8": 2 * B * N * Dm + 4 * B * N}
+        for fmt in ("fp16", "int8", "int4", "fp8"):
             ns = _nsets(per[fmt])
             sets = []
             err = None
@@ -428,12 +431,17 @@ def suite_mha_quant(torch, fq, steps, warmup, rows, shapes=None):
                     sets.append((Kq, Vq, Ks, Vs))
                     if k == 0:
                         Kf, Vf = quant.dequant_int8(Kq, Ks), quant.dequant_int8(Vq, Vs)
-                else:
+                elif fmt == "int4":
                     Kq, Ks = quant.quant_int4_per_token(Kx)
                     Vq, Vs = quant.quant_int4_per_token(Vx)
                     sets.append((Kq, Vq, Ks, Vs))
                     if k == 0:
                         Kf, Vf = quant.dequant_int4(Kq, Ks), quant.dequant_int4(Vq, Vs)
+                else:
+                    (Kq, Ks), (Vq, Vs) = fq.quantize_fp8_per_token(Kx), fq.quantize_fp8_per_token(Vx)
+                    sets.append((Kq.view(B, 1, N, Dm), Vq.view(B, 1, N, Dm), Ks.view(B, 1, N), Vs.view(B, 1, N)))
+                    if k == 0:
+                        Kf, Vf = quant.dequant_fp8(Kq, Ks), quant.dequant_fp8(Vq, Vs)
                 del Kx, Vx
             if fmt == "fp16":
                 fn = lambda i: fq.decode_attn_fp16_mw(q, sets[i][0], sets[i][1], W)
@@ -441,16 +449,20 @@ def suite_mha_quant(torch, fq, steps, warmup, rows, shapes=None):
             elif fmt == "int8":
                 fn = lambda i: fq.decode_attn_int8_mw(q, sets[i][0], sets[i][1], sets[i][2], sets[i][3], W)
                 nbytes = B * (2 * N * Dm + 4 * N + 4 * Dm)
-            else:
+            elif fmt == "int4":
                 fn = lambda i: fq.decode_attn_int4(q, sets[i][0], sets[i][1], sets[i][2], sets[i][3], W)
                 nbytes = B * (N * Dm + 4 * N + 4 * Dm)
+            else:
+                q1 = q.view(B, 1, Dm)
+                fn = lambda i: fq.decode_attn_gqa_fp8(q1, sets[i][0], sets[i][1], sets[i][2], sets[i][3], W).view(B, Dm)
+                nbytes = B * (2 * N * Dm + 4 * N + 4 * Dm)
             o = fn(0)
             ref = _ref_mha(torch, q, Kf, Vf)
             err = float((o.float() - ref).abs().max())
             del Kf, Vf, ref
             ms = _loop_ms(torch, fn, ns, steps, warmup)
             extra = {}
-            if Dm == 64:
+            if Dm == 64 and fmt != "fp8":
                 extra = {"ref_a100_us": REF_QUANT_D64_MS[B][("fp16", "int8", "int4").index(fmt)] * 1e3}
             rows.append(_row("mha_" + fmt, {"B": B, "N": N, "D": Dm, "W": W, "sets": ns}, ms, nbytes, err, **extra))
             log("%-10s B=%-5d N=%d D=%d  %9.2f us  %7.1f GB/s  err %.2e" % (fmt, B, N, Dm, ms * 1e3, nbytes / ms / 1e6, err))
@@ -573,10 +585,11 @@ def suite_splitk_quant(torch, fq, steps, warmup, rows):
     Hq, Hkv, Dd = 32, 8, 128
     G = Hq // Hkv
     for B, N in ((1, 16384), (8, 32768)):
-        for fmt in ("int8", "int4"):
+        for fmt in ("int8", "int4", "fp8"):
             g = torch.Generator(device="cuda").manual_seed(5)
-            quantize = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
-            per = (2 * B * Hkv * N * Dd if fmt == "int8" else B * Hkv * N * Dd) + 4 * B * Hkv * N
+            quantize = {"int8": fq.quantize_int8_per_token, "int4": fq.quantize_int4_per_token,
+                        "fp8": fq.quantize_fp8_per_token}[fmt]
+            per = (B * Hkv * N * Dd if fmt == "int4" else 2 * B * Hkv * N * Dd) + 4 * B * Hkv * N
             ns = _nsets(per)
             q = torch.randn(B * Hq, Dd, device="cuda", generator=g).half()
             sets = []
@@ -585,15 +598,13 @@ def suite_splitk_quant(torch, fq, steps, warmup, rows):
                 Vq, Vs = quantize(torch.randn(B * Hkv, N, Dd, device="cuda", generator=g))
                 sets.append((Kq, Vq, Ks, Vs))
             Kq, Vq, Ks, Vs = sets[0]
-            if fmt == "int8":
-                Kf, Vf = Kq.float() * Ks.float()[..., None], Vq.float() * Vs.float()[..., None]
-            else:
-                from fqkv_decode import quant
-                Kf, Vf = quant.dequant_int4(Kq, Ks), quant.dequant_int4(Vq, Vs)
+            from fqkv_decode import quant
+            deq = {"int8": quant.dequant_int8, "int4": quant.dequant_int4, "fp8": quant.dequant_fp8}[fmt]
+            Kf, Vf = deq(Kq, Ks), deq(Vq, Vs)
             ref = _ref_mha(torch, q, Kf.repeat_interleave(G, 0), Vf.repeat_interleave(G, 0))
             del Kf, Vf
-            f = fq.gqa_sk_fast_int8 if fmt == "int8" else fq.gqa_sk_fast_int4
-            nbytes = B * ((2 * Hkv * N * Dd if fmt == "int8" else Hkv * N * Dd) + 4 * Hkv * N + 4 * Hq * Dd)
+            f = {"int8": fq.gqa_sk_fast_int8, "int4": fq.gqa_sk_fast_int4, "fp8": fq.gqa_sk_fast_fp8}[fmt]
+            nbytes = B * ((Hkv * N * Dd if fmt == "int4" else 2 * Hkv * N * Dd) + 4 * Hkv * N + 4 * Hq * Dd)
             best = None
             for S in ((16, 32, 64) if B == 1 else (4, 8, 16)):
                 for W in (4, 8):

@@ -23,7 +23,7 @@ Usage::
 
 Quantized KV cache (no counterpart in the reference, whose hook keeps an fp16
 cache): :class:`QuantizedKVCache` stores every layer's keys and values in the
-int8 or int4 per-token format of ``fqkv_decode.quant``, quantizing new tokens
+int8, int4 or fp8 per-token format of ``fqkv_decode.quant``, quantizing new tokens
 with the GPU quantizer kernels, and the registered attention function runs
 decode steps on it with ``decode_attn_gqa_strided`` (the filled part of the
 preallocated cache is a strided view, read in place)::
@@ -45,7 +45,7 @@ model in a HIP graph and replays it per token::
 
     tokens = hf_llama.generate_graphed(model, ids, max_new_tokens=128)
 
-With ``kv_format="int8"`` or ``"int4"`` (on both) the static cache stores that
+With ``kv_format="int8"``, ``"int4"`` or ``"fp8"`` (on both) the static cache stores that
 per-token format; each step quantizes its new token into place with
 ``quantize_kv_append_at_``, which reads the position from the device, so the
 quantized cache is graph-replayed too.
@@ -57,6 +57,22 @@ import torch
 
 DEFAULT_NAME = "fqkv_decode"
 _W = 8  # waves per workgroup for the decode kernel
+_KV_FORMATS = ("int8", "int4", "fp8")
+
+
+def _code_storage(kv_format, D):
+    """(row width, dtype) of a quantized cache's code rows."""
+    return {"int8": (D, torch.int8), "int4": (D // 2, torch.uint8), "fp8": (D, torch.float8_e4m3fn)}[kv_format]
+
+
+def _dequant(codes, scales):
+    from . import quant
+
+    if codes.dtype == torch.int8:
+        return quant.dequant_int8(codes, scales)
+    if codes.dtype == torch.float8_e4m3fn:
+        return quant.dequant_fp8(codes, scales)
+    return quant.dequant_int4(codes, scales)
 
 
 def _sdpa(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
@@ -110,7 +126,7 @@ def _static_attention(module, query, key, value, attention_mask, scaling, dropou
     packed int4 carrying their fp16 scales [B, Hkv, capacity]): a decode step runs the paged kernel
     over the first seq_lens[b] tokens of sequence b's buffer (one page of ``capacity`` tokens; the
     lengths are read on the device); anything else goes to SDPA with transformers' mask (over the
-    dequantized cache for int8 / int4)."""
+    dequantized cache for int8 / int4 / fp8)."""
     B, Hq, qlen, D = query.shape
     ks, vs = getattr(key, "fqkv_scales", None), getattr(value, "fqkv_scales", None)
     # a caller's padding mask (folded into transformers' mask by the builder register() installs)
@@ -123,10 +139,7 @@ def _static_attention(module, query, key, value, attention_mask, scaling, dropou
           and (scaling is None or abs(scaling * math.sqrt(D) - 1.0) <= 1e-6))
     if not ok:
         if ks is not None:
-            from . import quant
-
-            deq = quant.dequant_int8 if key.dtype == torch.int8 else quant.dequant_int4
-            key, value = deq(key, ks).to(query.dtype), deq(value, vs).to(query.dtype)
+            key, value = _dequant(key, ks).to(query.dtype), _dequant(value, vs).to(query.dtype)
         return _sdpa(module, query, key, value, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
     from . import decode_attn_gqa_paged
 
@@ -138,8 +151,9 @@ def _static_attention(module, query, key, value, attention_mask, scaling, dropou
 
 
 def _quantized_attention(module, query, key, value, attention_mask, scaling, dropout, **kwargs):
-    """Attention over a QuantizedKVCache view: key/value are int8 (or packed uint8) [B, Hkv, kv, D or D/2]
-    views carrying their fp16 scales [B, Hkv, kv] as ``fqkv_scales``."""
+    """Attention over a QuantizedKVCache view: key/value are int8, packed uint8 (int4) or
+    float8_e4m3fn [B, Hkv, kv, D or D/2] views carrying their fp16 scales [B, Hkv, kv] as
+    ``fqkv_scales``."""
     ks, vs = key.fqkv_scales, value.fqkv_scales
     if not getattr(module, "training", False) and kernel_applies(query, key, attention_mask, scaling, dropout,
                                                                  **kwargs):
@@ -148,11 +162,8 @@ def _quantized_attention(module, query, key, value, attention_mask, scaling, dro
         q = query[:, :, 0, :].to(torch.float16).contiguous()
         out = decode_attn_gqa_strided(q, key, value, _W, ks, vs)
         return out.unsqueeze(1).to(query.dtype), None
-    from . import quant
-
-    deq = quant.dequant_int8 if key.dtype == torch.int8 else quant.dequant_int4
-    K = deq(key, ks).to(query.dtype)
-    V = deq(value, vs).to(query.dtype)
+    K = _dequant(key, ks).to(query.dtype)
+    V = _dequant(value, vs).to(query.dtype)
     return _sdpa(module, query, K, V, attention_mask, scaling=scaling, dropout=dropout, **kwargs)
 
 
@@ -166,7 +177,7 @@ def _make_layer_class():
     from transformers.cache_utils import DynamicLayer
 
     class QuantizedKVLayer(DynamicLayer):
-        """One decoder layer's KV cache in the kernels' int8 / int4 per-token format.
+        """One decoder layer's KV cache in the kernels' int8 / int4 / fp8 per-token format.
 
         Storage is preallocated [B, Hkv, capacity, D] int8 (or [.., D/2] packed
         uint8 for int4) plus [B, Hkv, capacity] fp16 scales, grown in blocks of
@@ -179,8 +190,8 @@ def _make_layer_class():
 
         def __init__(self, kv_format="int8", block=256):
             super().__init__()
-            if kv_format not in ("int8", "int4"):
-                raise ValueError("kv_format must be 'int8' or 'int4', got %r" % (kv_format,))
+            if kv_format not in _KV_FORMATS:
+                raise ValueError("kv_format must be 'int8', 'int4' or 'fp8', got %r" % (kv_format,))
             self.kv_format = kv_format
             self.block = block
             self.length = 0
@@ -195,7 +206,7 @@ def _make_layer_class():
             if need <= cap:
                 return
             cap = -(-max(need, 2 * cap) // self.block) * self.block
-            width, dt = (D, torch.int8) if self.kv_format == "int8" else (D // 2, torch.uint8)
+            width, dt = _code_storage(self.kv_format, D)
             k = torch.empty(B, H, cap, width, dtype=dt, device=self.device)
             v = torch.empty_like(k)
             ks = torch.empty(B, H, cap, dtype=torch.float16, device=self.device)
@@ -275,7 +286,7 @@ _LAYER_CLASS = None
 
 
 def QuantizedKVLayer(kv_format="int8", block=256):
-    """A transformers cache layer holding int8 / int4 KV (class built on first use)."""
+    """A transformers cache layer holding int8 / int4 / fp8 KV (class built on first use)."""
     global _LAYER_CLASS
     if _LAYER_CLASS is None:
         _LAYER_CLASS = _make_layer_class()
@@ -364,8 +375,8 @@ def _make_static_layer_class():
         their scales."""
 
         def __init__(self, max_cache_len, kv_format):
-            if kv_format not in ("int8", "int4"):
-                raise ValueError("kv_format must be 'int8' or 'int4', got %r" % (kv_format,))
+            if kv_format not in _KV_FORMATS:
+                raise ValueError("kv_format must be 'int8', 'int4' or 'fp8', got %r" % (kv_format,))
             super().__init__(max_cache_len)
             self.kv_format = kv_format
             self.prefilled = False
@@ -375,7 +386,7 @@ def _make_static_layer_class():
             self.batch_size, self.num_heads = key_states.shape[:2]
             B, H, D = self.batch_size, self.num_heads, key_states.shape[-1]
             self.k_head_dim = self.v_head_dim = D
-            width, dt = (D, torch.int8) if self.kv_format == "int8" else (D // 2, torch.uint8)
+            width, dt = _code_storage(self.kv_format, D)
             cap = self.max_cache_len
             self.keys = torch.zeros(B, H, cap, width, dtype=dt, device=self.device)
             self.values = torch.zeros_like(self.keys)
@@ -435,7 +446,7 @@ def StaticKVCache(config, max_cache_len, kv_format=None):
     (a power of two in [16, 2^20]) bounds prompt plus generated tokens. Decode steps on the kernel
     attend to the first ``length`` positions of each buffer and read no attention mask, so a call
     that passes a padding mask runs its decode steps on SDPA instead (still correct, not
-    graph-replayed by :func:`generate_graphed`, which passes none). ``kv_format`` "int8" or "int4"
+    graph-replayed by :func:`generate_graphed`, which passes none). ``kv_format`` "int8", "int4" or "fp8"
     stores the cache in that per-token format, quantized on the GPU as tokens arrive (the prompt
     attends to its exact states, later calls to the quantized cache)."""
     from transformers.cache_utils import Cache
@@ -460,7 +471,7 @@ def generate_graphed(model, input_ids, max_new_tokens, max_cache_len=None, use_g
     the paged kernel when the model's attention implementation is this module's), and writes its
     argmax back as the next step's input. The prompt rows are taken as unpadded (no attention mask
     is passed).
-    ``use_graph=False`` runs the same steps eagerly; ``kv_format`` "int8" / "int4" keeps the cache in
+    ``use_graph=False`` runs the same steps eagerly; ``kv_format`` "int8" / "int4" / "fp8" keeps the cache in
     that format (:func:`StaticKVCache`). Returns the new tokens, [B, max_new_tokens]."""
     B, L = input_ids.shape
     if max_new_tokens < 1:

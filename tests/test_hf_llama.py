@@ -36,6 +36,26 @@ def tiny_llama(layers=4, hidden=512, heads=8, kv_heads=2, head_dim=64, vocab=100
     return model.to(dtype).eval()
 
 
+def _quantizers():
+    from fqkv_decode import quant
+
+    return {"int8": quant.quant_int8_per_token, "int4": quant.quant_int4_per_token, "fp8": quant.quant_fp8_per_token}
+
+
+class _Lazy(dict):
+    def __missing__(self, k):
+        self.update(_quantizers())
+        return self[k]
+
+
+QUANTIZERS = _Lazy()  # kv_format -> fqkv_decode.quant's quantizer
+
+
+def bits(t):
+    """The bytes of a code tensor (float8 tensors compare through uint8)."""
+    return t.view(torch.uint8) if t.dtype == torch.float8_e4m3fn else t
+
+
 def set_impl(model, name):
     model.config._attn_implementation = name
     for layer in model.model.layers:
@@ -161,7 +181,7 @@ def _prefill(model, ids, cache):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("fmt", ["int8", "int4", "fp8"])
 def test_gpu_quantized_cache_stores_the_quantizer_bytes(fmt):
     """After a prefill, every layer holds exactly fqkv_decode.quant's bytes and scales of the
     prompt's keys and values (the prefill itself attends to the exact states)."""
@@ -177,16 +197,16 @@ def test_gpu_quantized_cache_stores_the_quantizer_bytes(fmt):
     logits = _prefill(model, ids, qc).logits
     assert torch.equal(logits, ref_logits)
     assert qc.get_seq_length() == 300
-    qfn = quant.quant_int8_per_token if fmt == "int8" else quant.quant_int4_per_token
+    qfn = QUANTIZERS[fmt]
     for lq, ld in zip(qc.layers, dyn.layers):
         for got, gs, x in ((lq._k, lq._ks, ld.keys), (lq._v, lq._vs, ld.values)):
             want, ws = qfn(x)
-            assert torch.equal(got[:, :, :300], want)
+            assert torch.equal(bits(got[:, :, :300]), bits(want))
             assert torch.equal(gs[:, :, :300], ws)
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("fmt", ["int8", "int4", "fp8"])
 def test_gpu_quantized_cache_decode_step(fmt, monkeypatch):
     """A decode step on the quantized cache. Attention level: the kernel on the strided
     cache view equals float32 attention over the dequantized cache (max-abs 2e-3 relative
@@ -223,7 +243,7 @@ def test_gpu_quantized_cache_decode_step(fmt, monkeypatch):
     k, v = qc.layers[0]._views()
     q = torch.randn(1, 8, 1, 64, device="cuda", generator=torch.Generator(device="cuda").manual_seed(0)).half()
     o, _ = hf_llama.attention_forward(model.model.layers[0].self_attn, q, k, v, None, scaling=1 / 8)
-    deq = quant.dequant_int8 if fmt == "int8" else quant.dequant_int4
+    deq = hf_llama._dequant
     Kf = deq(k, k.fqkv_scales).float().repeat_interleave(4, 1)
     Vf = deq(v, v.fqkv_scales).float().repeat_interleave(4, 1)
     ref = torch.softmax(q.float() @ Kf.transpose(-1, -2) / 8, -1) @ Vf
@@ -262,7 +282,7 @@ def test_static_cache_rejects_a_capacity_the_kernel_cannot_page():
             hf_llama.StaticKVCache(cfg, bad)
     assert len(hf_llama.StaticKVCache(cfg, 64).layers) == 2
     with pytest.raises(ValueError, match="kv_format"):
-        hf_llama.StaticKVCache(cfg, 64, "fp8")
+        hf_llama.StaticKVCache(cfg, 64, "fp4")
     assert len(hf_llama.StaticKVCache(cfg, 64, "int4").layers) == 2
 
 
@@ -398,7 +418,7 @@ def test_gpu_static_cache_with_a_padding_mask_goes_to_sdpa(monkeypatch):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("fmt", ["int8", "int4", "fp8"])
 def test_gpu_static_quantized_cache_prefill_and_decode(fmt):
     """StaticKVCache(kv_format=int8 / int4): the prompt attends to its exact states (logits equal
     the dynamic fp16 cache's), the buffers hold fqkv_decode.quant's bytes and scales of the
@@ -419,13 +439,13 @@ def test_gpu_static_quantized_cache_prefill_and_decode(fmt):
     ref_logits = _prefill(model, ids, dyn).logits
     sc = hf_llama.StaticKVCache(model.config, 512, fmt)
     assert torch.equal(_prefill(model, ids, sc).logits, ref_logits)
-    qfn = quant.quant_int8_per_token if fmt == "int8" else quant.quant_int4_per_token
+    qfn = QUANTIZERS[fmt]
     for ls, ld in zip(sc.layers, dyn.layers):
         assert ls.seq_lens.tolist() == [L, L]
         for got, gs, x in ((ls.keys, ls.key_scales, ld.keys), (ls.values, ls.value_scales, ld.values)):
             want, ws = qfn(x)
-            assert torch.equal(got[:, :, :L], want) and torch.equal(gs[:, :, :L], ws)
-            assert not got[:, :, L:].any() and not gs[:, :, L:].any()
+            assert torch.equal(bits(got[:, :, :L]), bits(want)) and torch.equal(gs[:, :, :L], ws)
+            assert not bits(got[:, :, L:]).any() and not gs[:, :, L:].any()
 
     nxt = ref_logits[:, -1:].argmax(-1)
     qc = hf_llama.QuantizedKVCache(model.config, fmt)
@@ -448,7 +468,7 @@ def test_gpu_static_quantized_cache_prefill_and_decode(fmt):
     q = torch.randn(2, 8, 1, 64, device="cuda", generator=torch.Generator(device="cuda").manual_seed(1)).half()
     o, _ = hf_llama.attention_forward(model.model.layers[0].self_attn, q, layer.keys, layer.values, None,
                                       scaling=1 / 8)
-    deq = quant.dequant_int8 if fmt == "int8" else quant.dequant_int4
+    deq = hf_llama._dequant
     n = L + 1
     Kf = deq(layer.keys[:, :, :n], layer.key_scales[:, :, :n]).float().repeat_interleave(4, 1)
     Vf = deq(layer.values[:, :, :n], layer.value_scales[:, :, :n]).float().repeat_interleave(4, 1)
@@ -481,15 +501,15 @@ def test_gpu_static_quantized_cache_reorders_scales_and_lengths():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("fmt", ["int8", "int4"])
+@pytest.mark.parametrize("fmt", ["int8", "int4", "fp8"])
 def test_gpu_graphed_generation_quantized(fmt, monkeypatch):
-    """generate_graphed over an int8 / int4 static cache: each token is appended by the
+    """generate_graphed over an int8 / int4 / fp8 static cache: each token is appended by the
     device-position quantizer and attended by the paged kernel with scale pages, in the captured
     step too. Replayed tokens equal the eager steps bit for bit, and the greedy tokens over the
     dynamic quantized cache (int8: a divergence only where that run's top-2 margin is below 2e-2;
-    int4 is left out of that comparison, since a last-bit difference between two kernels can move
-    a later token across one of the quantizer's wide rounding steps and the greedy paths apart; its
-    per-step agreement is the test above)."""
+    int4 and fp8 are left out of that comparison, since a last-bit difference between two kernels
+    can move a later token across one of the quantizer's wide rounding steps and the greedy paths
+    apart; their per-step agreement is the test above)."""
     name = hf_llama.register()
     model = tiny_llama(dtype=torch.float16, device="cuda")
     set_impl(model, name)
@@ -513,7 +533,7 @@ def test_gpu_graphed_generation_quantized(fmt, monkeypatch):
     assert n_eager == 39 * layers
     assert calls["n"] - n_eager == 2 * layers
     assert torch.equal(graphed, eager)
-    if fmt == "int4":
+    if fmt != "int8":
         return
     for i, (a, b) in enumerate(zip(base, graphed[0].tolist())):
         if a != b:
