@@ -157,8 +157,8 @@ int fqkv_gqa_sk_fast_noalloc(const void* q, const void* K, const void* V, void* 
                              int64_t N, int64_t D, int64_t S, int64_t W, int64_t CW, void* stream);
 
 /*
- * GQA-aware decode over an int8 or int4 KV cache (kv_format FQKV_KV_I8 /
- * FQKV_KV_I4) with per-token fp16 scales: the GQA head mapping of
+ * GQA-aware decode over an int8, int4 or fp8 e4m3 KV cache (kv_format
+ * FQKV_KV_I8 / FQKV_KV_I4 / FQKV_KV_FP8, fp8 laid out as int8) with per-token fp16 scales: the GQA head mapping of
  * fqkv_decode_attn_gqa with the KV format of fqkv_decode_attn_int8_mw /
  * fqkv_decode_attn_int4. q: [B, Hq, D] fp16; K, V: [B, Hkv, N, D] int8 or
  * [B, Hkv, N, D/2] uint8; Ks, Vs: [B, Hkv, N] fp16; o: [B, Hq, D] fp16.
@@ -172,7 +172,7 @@ int fqkv_decode_attn_gqa_quant(const void* q, const void* K, const void* V, cons
                                size_t workspace_bytes, void* stream);
 
 /*
- * GQA split-K decode over an int8 or int4 KV cache: fqkv_gqa_sk_fast with K,
+ * GQA split-K decode over an int8, int4 or fp8 KV cache: fqkv_gqa_sk_fast with K,
  * V in the quantized layout above and per-token scales Ks, Vs [Hkv, N] fp16
  * (batch folded into the head axis as for fqkv_gqa_sk_fast). Same scratch
  * layout and semantics. No counterpart in the reference (its split-K path,
@@ -276,6 +276,11 @@ int fqkv_dequant_kv(const void* Kq, const void* Ks, float* out, int64_t tokens, 
  * (int8 D 128 / int8 D 64 or int4 D 128 / int4 D 64), scales 2 bytes.
  * Replaces the PyTorch quantizers qpt (tests/test_kernels.py:32-34) and
  * quant_int4_per_token (nb:292-299), which run on the CPU in the reference.
+ * kv_format FQKV_KV_FP8 (no counterpart in the reference) writes fp8 e4m3
+ * codes [tokens, D] instead, in fp32 for every source type: s = max(max|x| *
+ * fp32(1/448), 1e-8), code = e4m3 round-to-nearest-even of clamp(x / s,
+ * +-448), an exact zero as +0, scale fp16(s). bf16 sources (FQKV_SRC_BF16)
+ * follow the fp32 expressions for every format.
  */
 int fqkv_quantize_kv(const void* X, int x_dtype, void* Q, void* scales, int64_t tokens, int64_t D,
                      int kv_format, void* stream);

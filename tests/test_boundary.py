@@ -204,6 +204,9 @@ def test_capi_quantized_gqa_and_split_reject_bad_args(lib):
     fs.argtypes = [VP] * 9 + [I64] * 4 + [ctypes.c_int, I64, I64, I64, VP]
     assert fs(*[16] * 9, 32, 8, 64, 128, 1, 16, 8, 3, None) == 1 and _err(lib).startswith("CW:")
     assert fs(*[16] * 9, 32, 8, 64, 128, 0, 16, 8, 4, None) == 1 and "kv_format" in _err(lib)
+    # fp8 (kv_format 4) is accepted, so the next check speaks; 5 is unknown
+    assert fs(*[16] * 9, 32, 8, 64, 128, 4, 0, 8, 4, None) == 1 and _err(lib).startswith("S:")
+    assert fs(*[16] * 9, 32, 8, 64, 128, 5, 16, 8, 4, None) == 1 and "kv_format" in _err(lib)
     assert fs(*[16] * 9, 32, 8, 64, 128, 2, 0, 8, 4, None) == 1 and _err(lib).startswith("S:")
 
 
