@@ -399,7 +399,7 @@ def _ref_mha(torch, q, Kf, Vf):
 REF_QUANT_D64_MS = {8: (0.2263, 0.2478, 0.2662), 256: (0.4792, 0.4864, 0.4915), 2048: (2.0951, 1.6814, 1.5585)}
 
 
-def suite_mha_quant(torch, fq, steps, warmup, rows, shapes=None):
+def suite_mha_quant(torch, fq, steps, warmup, rows, shapes=None, formats=("fp16", "int8", "int4", "fp8")):
     """fp16 / int8 / int4 MHA decode at B in {8, 256, 2048}, N=4096, W=8, at D=128 and at the
     reference's own D=64 (its A100 numbers alongside); fp8 (no counterpart in the reference)
     through decode_attn_gqa_fp8 with one query head per KV head; shapes: (D, B) pairs to run
@@ -413,7 +413,7 @@ def suite_mha_quant(torch, fq, steps, warmup, rows, shapes=None):
         q = torch.randn(B, Dm, device="cuda", generator=g).half()
         per = {"fp16": 2 * B * N * Dm * 2, "int8": 2 * B * N * Dm + 4 * B * N, "int4": B * N * Dm + 4 * B * N,
                "fp8": 2 * B * N * Dm + 4 * B * N}
-        for fmt in ("fp16", "int8", "int4", "fp8"):
+        for fmt in formats:
             ns = _nsets(per[fmt])
             sets = []
             err = None
@@ -946,7 +946,8 @@ def reference_tables(torch, fq):
     Each row is gated against fp32 PyTorch on the GPU (max-abs <= 2e-3), loop-timed like the
     suite (400 calls after 40 warm-ups); the reference's A100 numbers ride along."""
     rows = []
-    suite_mha_quant(torch, fq, 400, 40, rows, shapes=[(64, b) for b in (8, 256, 2048)])
+    suite_mha_quant(torch, fq, 400, 40, rows, shapes=[(64, b) for b in (8, 256, 2048)],
+                    formats=("fp16", "int8", "int4"))
     sq = {}
     for r in rows:
         fmt, B = r["bench"].split("_")[1], r["config"]["B"]
