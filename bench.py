@@ -894,17 +894,17 @@ def suite_llama(torch, fq, rows, full=True):
         for impl, key in ((name, "kernel"), ("sdpa", "sdpa")):
             r["graphed_step_ms_%s_ctx%d" % (key, ctx)] = round(
                 (graphed_s(impl, ctx, 256) - graphed_s(impl, ctx, 128)) / 128 * 1e3, 4)
-    # the same hook over an int8 / int4 KV cache (hf_llama.QuantizedKVCache); KV bytes read per
-    # decode step at 8192 cached tokens: 16 layers x 2 x 8 heads x 8192 x (128, 64 + 2, 32 + 2) B
-    for fmt in ("int8", "int4"):
+    # the same hook over an int8 / int4 / fp8 KV cache (hf_llama.QuantizedKVCache); KV bytes read
+    # per decode step at 8192 cached tokens: 16 layers x 2 x 8 heads x 8192 x (128, 64 + 2, 32 + 2) B
+    for fmt in ("int8", "int4", "fp8"):
         r["kernel_%s_tok_s" % fmt] = round(tok_per_s(name, kv_format=fmt), 2)
         r["decode_ms_kernel_%s_ctx8192" % fmt] = round(decode_ms(name, 8192, kv_format=fmt), 4)
-        # graph-replayed over a static int8 / int4 cache (device-position append + paged kernel)
+        # graph-replayed over a static quantized cache (device-position append + paged kernel)
         r["kernel_graphed_%s_tok_s" % fmt] = round(128 / graphed_s(name, 512, 128, kv_format=fmt), 2)
         r["graphed_step_ms_kernel_%s_ctx8192" % fmt] = round(
             (graphed_s(name, 8192, 256, kv_format=fmt) - graphed_s(name, 8192, 128, kv_format=fmt)) / 128 * 1e3, 4)
     r["kv_mb_per_step_ctx8192"] = {f: round(16 * 2 * 8 * 8192 * b / 1e6, 1)
-                                   for f, b in (("fp16", 128), ("int8", 66), ("int4", 34))}
+                                   for f, b in (("fp16", 128), ("int8", 66), ("int4", 34), ("fp8", 66))}
     rows.append(r)
     log("llama     generate tok/s: sdpa %.2f, kernel %.2f; decode step ms (sdpa/kernel) ctx512 %.3f/%.3f "
         "ctx2048 %.3f/%.3f ctx8192 %.3f/%.3f" % (r["sdpa_tok_s"], r["kernel_tok_s"], r["decode_ms_sdpa_ctx512"],
@@ -916,11 +916,11 @@ def suite_llama(torch, fq, rows, full=True):
                                                 r["graphed_step_ms_sdpa_ctx512"], r["graphed_step_ms_kernel_ctx512"],
                                                 r["graphed_step_ms_sdpa_ctx8192"],
                                                 r["graphed_step_ms_kernel_ctx8192"]))
-    log("llama     int8 / int4 KV cache: generate tok/s %.2f / %.2f; decode step ms ctx8192 %.3f / %.3f; "
-        "graphed tok/s %.2f / %.2f, replayed step ms ctx8192 %.3f / %.3f"
-        % (r["kernel_int8_tok_s"], r["kernel_int4_tok_s"], r["decode_ms_kernel_int8_ctx8192"],
-           r["decode_ms_kernel_int4_ctx8192"], r["kernel_graphed_int8_tok_s"], r["kernel_graphed_int4_tok_s"],
-           r["graphed_step_ms_kernel_int8_ctx8192"], r["graphed_step_ms_kernel_int4_ctx8192"]))
+    for fmt in ("int8", "int4", "fp8"):
+        log("llama     %s KV cache: generate tok/s %.2f; decode step ms ctx8192 %.3f; graphed tok/s %.2f, "
+            "replayed step ms ctx8192 %.3f" % (fmt, r["kernel_%s_tok_s" % fmt], r["decode_ms_kernel_%s_ctx8192" % fmt],
+                                                r["kernel_graphed_%s_tok_s" % fmt],
+                                                r["graphed_step_ms_kernel_%s_ctx8192" % fmt]))
     set_impl("sdpa")
     del model
     torch.cuda.empty_cache()
