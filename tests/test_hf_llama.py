@@ -594,3 +594,26 @@ def test_gpu_bf16_model_decodes_on_the_kernel(monkeypatch):
     graphed = hf_llama.generate_graphed(model, ids[:1, :45], 20)
     assert n == 19 * 2 and calls["paged"] - n == 2 * 2
     assert torch.equal(graphed, eager)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+def test_gpu_bf16_model_quantized_cache(fmt):
+    """A bf16 model over an int8 / fp8 cache: the layers hand their bf16 keys and values to the
+    quantizer as they are (no conversion pass), which quantizes them as their fp32 values, so the
+    cache holds fqkv_decode.quant's bytes of x.float(); a decode step then runs on the kernel."""
+    name = hf_llama.register()
+    model = tiny_llama(layers=2, dtype=torch.bfloat16, device="cuda")
+    set_impl(model, name)
+    ids = torch.randint(0, 1000, (2, 100), generator=torch.Generator().manual_seed(14)).cuda()
+    dyn = transformers.DynamicCache(config=model.config)
+    _prefill(model, ids, dyn)
+    qc = hf_llama.QuantizedKVCache(model.config, fmt)
+    _prefill(model, ids, qc)
+    for lq, ld in zip(qc.layers, dyn.layers):
+        for got, gs, x in ((lq._k, lq._ks, ld.keys), (lq._v, lq._vs, ld.values)):
+            want, ws = QUANTIZERS[fmt](x.float())
+            assert torch.equal(bits(got[:, :, :100]), bits(want)) and torch.equal(gs[:, :, :100], ws)
+    with torch.no_grad():
+        out = model(ids[:, :1], past_key_values=qc, use_cache=True).logits
+    assert out.dtype == torch.bfloat16 and torch.isfinite(out.float()).all()
