@@ -213,7 +213,8 @@ def test_capi_quantized_gqa_and_split_reject_bad_args(lib):
 def test_binding_exposes_quantized_and_quantizer_entry_points():
     for name in ("decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8", "gqa_sk_fast_int4",
                  "quantize_int8_per_token", "quantize_int4_per_token", "decode_attn_gqa_nhd",
-                 "decode_attn_gqa_strided", "decode_attn_gqa_paged"):
+                 "decode_attn_gqa_strided", "decode_attn_gqa_paged", "decode_attn_gqa_fp8", "gqa_sk_fast_fp8",
+                 "quantize_fp8_per_token", "quantize_kv_append_", "quantize_kv_append_at_", "quantize_kv_to_pages_"):
         assert callable(getattr(fqkv_decode, name))
     with pytest.raises(RuntimeError, match="^cuda"):
         fqkv_decode.quantize_int8_per_token(torch.zeros(4, 128))
