@@ -181,3 +181,21 @@ def test_entry_points_reject_other_dtypes():
     s = torch.zeros(1, 8, 16, dtype=torch.float16, device=DEV)
     with pytest.raises(RuntimeError, match="^fp8"):
         fq.decode_attn_gqa_fp8(q, K, K, s, s, 8)
+
+
+@pytest.mark.parametrize("D,B", [(64, 8), (64, 2), (128, 8)])
+def test_token_major_layout(D, B):
+    """Token-major [B, N, Hkv, D] fp8 caches: at D 64 a token's row is 64 bytes, so neighbouring
+    KV heads share 128-byte lines and the launcher's head grouping renumbers the work items; the
+    output equals the head-major layout's bit for bit, and the oracle."""
+    g = torch.Generator().manual_seed(86 + D + B)
+    Hq, Hkv, N = 32, 8, 2000
+    q = draw(g, B, Hq, D).half()
+    Kq, Ks, Kf = quantize(draw(g, B, N, Hkv, D))
+    Vq, Vs, Vf = quantize(draw(g, B, N, Hkv, D))
+    out = fq.decode_attn_gqa_nhd(q.to(DEV), Kq, Vq, 8, Ks, Vs)
+    hm = lambda t: t.transpose(1, 2).contiguous()
+    ref_c = fq.decode_attn_gqa_fp8(q.to(DEV), hm(Kq.view(torch.uint8)).view(torch.float8_e4m3fn),
+                                   hm(Vq.view(torch.uint8)).view(torch.float8_e4m3fn), hm(Ks), hm(Vs), 8)
+    assert torch.equal(out, ref_c)
+    assert maxerr(out, oracle.gqa_attention(q.numpy(), Kf.transpose(0, 2, 1, 3), Vf.transpose(0, 2, 1, 3))) <= TOL
