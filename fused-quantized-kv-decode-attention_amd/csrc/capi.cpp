@@ -529,8 +529,8 @@ int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const vo
                            float* m_part, float* l_part, float* o_part, void* o, int64_t Hq,
                            int64_t Hkv, int64_t N, int64_t D, int kv_format, int64_t S, int64_t W,
                            int64_t CW, void* stream) {
-  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4 && kv_format != FQKV_KV_FP8)
-    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8, FQKV_KV_I4 or FQKV_KV_FP8");
+  if (kv_format != FQKV_KV_I8 && kv_format != FQKV_KV_I4 && kv_format != FQKV_KV_FP8 && kv_format != FQKV_KV_BF16)
+    return fail(FQKV_ERR_ARG, "kv_format must be FQKV_KV_I8, FQKV_KV_I4, FQKV_KV_FP8 or FQKV_KV_BF16");
   return sk_fast(kv_format, q, K, V, Ks, Vs, m_part, l_part, o_part, o, Hq, Hkv, N, D, S, W, CW, stream,
                  nullptr, nullptr);
 }

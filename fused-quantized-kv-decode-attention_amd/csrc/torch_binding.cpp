@@ -206,6 +206,22 @@ void sk_checks(const torch::Tensor& q, const torch::Tensor& K, const torch::Tens
   TORCH_CHECK(o.numel() == Hq * D, "combine: o must hold Hq*D = ", Hq * D, " halves");
 }
 
+// gqa_sk_fast_bf16: gqa_sk_fast over bf16 K and V [Hkv,N,D] (q, o fp16), the same scratch; no
+// counterpart in the reference (its split-K is fp16 only).
+void gqa_sk_fast_bf16(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor m_part, torch::Tensor l_part,
+                      torch::Tensor o_part, torch::Tensor o, int64_t S, int64_t W, int64_t CW) {
+  TORCH_CHECK(K.scalar_type() == torch::kBFloat16 && V.scalar_type() == torch::kBFloat16,
+              "bf16: K and V must be bfloat16");
+  // the fp16 checks with K and V standing in as fp16 views of the same shape
+  sk_checks(q, K.view(torch::kHalf), V.view(torch::kHalf), m_part, l_part, o_part, o, S, W, CW);
+  const c10::DeviceGuard guard(q.device());
+  check_rc(fqkv_gqa_sk_fast_quant(q.data_ptr(), K.data_ptr(), V.data_ptr(), nullptr, nullptr,
+                                  m_part.data_ptr<float>(), l_part.data_ptr<float>(), o_part.data_ptr<float>(),
+                                  o.data_ptr(), q.size(0), K.size(0), K.size(1), q.size(1), FQKV_KV_BF16, S, W, CW,
+                                  cur_stream(q)),
+           "launch");
+}
+
 // gqa_sk_fast(q[Hq,D], K[Hkv,N,D], V, m_part[Hq,S], l_part[Hq,S], o_part[Hq,S,D], o[Hq,D], S, W, CW)
 void gqa_sk_fast(torch::Tensor q, torch::Tensor K, torch::Tensor V, torch::Tensor m_part, torch::Tensor l_part,
                  torch::Tensor o_part, torch::Tensor o, int64_t S, int64_t W, int64_t CW) {
@@ -708,6 +724,9 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
   m.def("gqa_sk_fast_int4", &gqa_sk_fast_int4, "GQA split-K int4-KV decode", py::arg("q"), py::arg("K"),
         py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("m_part"), py::arg("l_part"), py::arg("o_part"),
         py::arg("o"), py::arg("S"), py::arg("W"), py::arg("CW"));
+  m.def("gqa_sk_fast_bf16", &gqa_sk_fast_bf16, "GQA split-K decode over bf16 K and V", py::arg("q"), py::arg("K"),
+        py::arg("V"), py::arg("m_part"), py::arg("l_part"), py::arg("o_part"), py::arg("o"), py::arg("S"),
+        py::arg("W"), py::arg("CW"));
   m.def("decode_attn_gqa_fp8", &decode_attn_gqa_fp8, "GQA-aware fp8 (e4m3) KV decode", py::arg("q"), py::arg("K"),
         py::arg("V"), py::arg("Ks"), py::arg("Vs"), py::arg("W"));
   m.def("gqa_sk_fast_fp8", &gqa_sk_fast_fp8, "GQA split-K fp8 (e4m3) KV decode", py::arg("q"), py::arg("K"),

@@ -69,6 +69,7 @@ __all__ = [
     "quantize_int8_per_token",
     "quantize_int4_per_token",
     "decode_attn_gqa_fp8",
+    "gqa_sk_fast_bf16",
     "gqa_sk_fast_fp8",
     "quantize_fp8_per_token",
     "quantize_kv_append_",
@@ -85,7 +86,7 @@ __all__ = [
 _ENTRY_POINTS = ("decode_attn_fp16_mw", "decode_attn_int8_mw", "decode_attn_int4", "decode_attn_gqa",
                  "gqa_sk_fast", "decode_attn_gqa_int8", "decode_attn_gqa_int4", "gqa_sk_fast_int8",
                  "gqa_sk_fast_int4", "quantize_int8_per_token", "quantize_int4_per_token", "decode_attn_gqa_fp8",
-                 "gqa_sk_fast_fp8", "quantize_fp8_per_token", "quantize_kv_append_",
+                 "gqa_sk_fast_fp8", "quantize_fp8_per_token", "gqa_sk_fast_bf16", "quantize_kv_append_",
                  "quantize_kv_append_at_", "quantize_kv_to_pages_", "decode_attn_gqa_nhd", "decode_attn_gqa_strided", "decode_attn_gqa_paged")
 _EXT = None
 

@@ -176,7 +176,8 @@ int fqkv_decode_attn_gqa_quant(const void* q, const void* K, const void* V, cons
  * V in the quantized layout above and per-token scales Ks, Vs [Hkv, N] fp16
  * (batch folded into the head axis as for fqkv_gqa_sk_fast). Same scratch
  * layout and semantics. No counterpart in the reference (its split-K path,
- * decode_attn_gqa_sk_fast.cu:95-112, is fp16 only).
+ * decode_attn_gqa_sk_fast.cu:95-112, is fp16 only). kv_format FQKV_KV_BF16
+ * takes bf16 K, V [Hkv, N, D] instead (Ks, Vs ignored).
  */
 int fqkv_gqa_sk_fast_quant(const void* q, const void* K, const void* V, const void* Ks, const void* Vs,
                            float* m_part, float* l_part, float* o_part, void* o, int64_t Hq,

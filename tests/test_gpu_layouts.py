@@ -286,3 +286,21 @@ def test_bf16_keys_beyond_the_fp16_range():
     ref = oracle.gqa_attention(q.numpy(), K.float().numpy(), V.float().numpy())
     assert np.isfinite(out.float().cpu().numpy()).all()
     assert maxerr(out, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("N,D,S", [(16384, 128, 32), (100, 64, 7), (3, 128, 8)])
+def test_bf16_split_k_with_caller_scratch(N, D, S):
+    """gqa_sk_fast_bf16: the reference's split-K call (caller-owned scratch) with bf16 K and V,
+    against the oracle; fp16 K and V are refused."""
+    g = torch.Generator().manual_seed(60 + N)
+    Hq, Hkv = 32, 8
+    q = draw(g, Hq, D).half()
+    K, V = draw(g, Hkv, N, D).bfloat16(), draw(g, Hkv, N, D).bfloat16()
+    mp, lp = torch.empty(Hq, S, device="cuda"), torch.empty(Hq, S, device="cuda")
+    op = torch.empty(Hq, S, D, device="cuda")
+    o = torch.empty(Hq, D, dtype=torch.float16, device="cuda")
+    fq.gqa_sk_fast_bf16(q.cuda(), K.cuda(), V.cuda(), mp, lp, op, o, S, 8, 8)
+    Kf, Vf = K.float().numpy(), V.float().numpy()
+    assert maxerr(o, oracle.gqa_attention(q.numpy()[None], Kf[None], Vf[None])[0]) <= TOL
+    with pytest.raises(RuntimeError, match="^bf16"):
+        fq.gqa_sk_fast_bf16(q.cuda(), K.half().cuda(), V.half().cuda(), mp, lp, op, o, S, 8, 8)
