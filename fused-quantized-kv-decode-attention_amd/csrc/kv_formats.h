@@ -215,8 +215,8 @@ struct Fmt<KV_F16, D> {
 // ---------------------------------------------------------------- bf16 ----
 // bf16 K and V move exactly like fp16 (16-bit elements: the same loads, LDS
 // staging and exchanges, the same bit patterns in the operand registers); only
-// the matrix-core products differ, which take bf16 operands (the query and
-// the weights as bf16 pairs, hi + lo, so neither loses precision).
+// the matrix-core products differ, which take bf16 operands: the query as a
+// bf16 pair hi + lo (exact) and the weights as one (to 2^-16 relative).
 template <int D>
 struct Fmt<KV_BF16, D> : Fmt<KV_F16, D> {
   static constexpr bool BF16 = true;
