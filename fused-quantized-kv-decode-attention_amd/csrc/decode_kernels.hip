@@ -42,8 +42,8 @@
 // Two formats beyond the reference's ride the same code: bf16 rows move like
 // fp16 and take the bf16 matrix-core product (the query and the weights as
 // bf16 pairs: the query exact, the weights to 2^-16), and fp8 e4m3 codes move
-// like int8 and convert to exact
-// fp16 in hardware (no bias: per-token scales only).
+// like int8 and convert to exact fp16 in hardware (no bias: per-token scales
+// only).
 //
 // Reference algorithm: decode_attn_gqa_sk_fast.cu:6-54 (partial),
 // :57-94 (combine); decode_attn_fp16_mw.cu:6-49 and decode_attn_gqa.cu:8-55
