@@ -21,6 +21,9 @@ Beyond the reference (same conventions, no counterpart there):
     decode_attn_gqa_fp8 / gqa_sk_fast_fp8 / quantize_fp8_per_token
                                                     the same over OCP fp8 e4m3 codes
                                                     (float8_e4m3fn) with fp16 per-token scales
+    gqa_sk_fast_bf16(q, K[Hkv,N,D] bf16, V, m_part, l_part, o_part, o, S, W, CW)
+                                                    split-K over a bf16 cache (the layout entry
+                                                    points below take bf16 K and V as well)
     quantize_kv_append_(K_new[B,H,n,D], V_new, K_cache[B,H,cap,D or D/2], V_cache,
         Ks_cache[B,H,cap], Vs_cache, pos) -> None  the quantizers in append form for a live
                                                     cache: one launch, in place at pos
