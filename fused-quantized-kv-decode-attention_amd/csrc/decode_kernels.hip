@@ -52,6 +52,7 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include <atomic>
 #include <numeric>
@@ -529,7 +530,13 @@ __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const f
       const size_t b = qh * p.S + s;
       float* orow = p.o_part + b * D;
       const float mo = (M == -INFINITY) ? -INFINITY : M * p.scale;
-      if (p.slot >= 0) {  // device-scope stores: read by another workgroup of this launch
+      if (p.slot >= 0 && p.xcd_local) {  // read by a workgroup on this XCD: its L2 is the meeting point
+        if (d == 0) {
+          __hip_atomic_store(p.m_part + b, mo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          __hip_atomic_store(p.l_part + b, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+        __hip_atomic_store(orow + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      } else if (p.slot >= 0) {  // device-scope stores: read by another workgroup of this launch
         if (d == 0) {
           __hip_atomic_store(p.m_part + b, mo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           __hip_atomic_store(p.l_part + b, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1171,22 +1178,38 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // visible device-wide. The last arriver reads every partial with
   // device-scope loads. No L2 writeback or invalidate is needed, and nobody
   // waits on the counter, so no workgroup can stall.
+  //
+  // When the host has found that every workgroup of a group runs on one XCD
+  // (p.xcd_local: the XCD of a workgroup is fixed by blockIdx.x mod the XCD
+  // count, and split-major order gives a group the same residue for every
+  // split), that XCD's L2 is coherent for all of them: the partials, the
+  // counter and the merge's loads stay in it (workgroup-scope stores write
+  // through the CU's L1 to the L2, the store acknowledgements come from the
+  // L2, the counter's atomic executes there, and the merge's sc0 loads skip
+  // the merging CU's L1), as on a GPU with one L2.
   FQKV_STAMP(6);  // output or partials issued
   if (!p.direct && p.slot >= 0) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (threadIdx.x == 0) {
-      int* ctr = arrival_counter(p.slot, wsg);
-      s_last = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == p.S - 1;
-    }
+    int* ctr = arrival_counter(p.slot, wsg);
+    if (threadIdx.x == 0)
+      s_last = (p.xcd_local ? __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                            : __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) == p.S - 1;
     __syncthreads();
     FQKV_STAMP(7);  // arrival known
     if (s_last) {
-      merge_splits<D, CPOL_SC1>(p.m_part, p.l_part, p.o_part, p.o, qrow0, hcnt, p.S, s_mw, s_mr);
+      if (p.xcd_local)
+        merge_splits<D, CPOL_SC0>(p.m_part, p.l_part, p.o_part, p.o, qrow0, hcnt, p.S, s_mw, s_mr);
+      else
+        merge_splits<D, CPOL_SC1>(p.m_part, p.l_part, p.o_part, p.o, qrow0, hcnt, p.S, s_mw, s_mr);
       FQKV_STAMP(9);  // merge done
       // every workgroup of the group has counted in: reset for the next call
-      if (threadIdx.x == 0)
-        __hip_atomic_store(arrival_counter(p.slot, wsg), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0) {
+        if (p.xcd_local)
+          __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        else
+          __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
   FQKV_STAMP(10);  // end
@@ -1244,6 +1267,58 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
 }
 
 // ------------------------------------------------------------ launchers ----
+// XCD period of a device: the workgroups of a launch are dealt to the XCDs
+// round-robin by blockIdx.x. A one-time probe records every workgroup's XCC_ID
+// (hardware register 20, bits 3:0) over 4096 workgroups and accepts n >= 2
+// only if the first n workgroups sit on n distinct XCDs and workgroup i on the
+// XCD of workgroup i mod n; otherwise (a register that reads one value, any
+// other order) the split merge keeps its device-scope protocol.
+constexpr int XCC_PROBE_BLOCKS = 4096;
+constexpr int XCC_ID_HWREG = (3 << 11) | 20;  // s_getreg operand: 4 bits at offset 0 of register 20
+static __device__ __align__(256) uint32_t g_xcc_ids[XCC_PROBE_BLOCKS];
+static std::atomic<int> g_xcd_period[64];  // 0: not probed, -1: not usable, n: period
+
+__global__ void __launch_bounds__(64) xcc_record_kernel(uint32_t* ids) {
+  if (threadIdx.x == 0) ids[blockIdx.x] = (uint32_t)__builtin_amdgcn_s_getreg(XCC_ID_HWREG) & 15u;
+}
+
+// Probed on the first eager call per device (a stream that is capturing gets
+// 0, the device-scope protocol, and leaves the probe for later); reads the
+// 16 KiB of ids back on the caller's stream. Allocates nothing.
+static int xcd_period(hipStream_t st) {
+  int dev = 0, cur = 0;
+  if ((st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev)) != hipSuccess || hipGetDevice(&cur) != hipSuccess ||
+      dev != cur || dev < 0 || dev >= 64)
+    return 0;
+  const int known = g_xcd_period[dev].load(std::memory_order_acquire);
+  if (known != 0) return known > 0 ? known : 0;
+  if (st == hipStreamPerThread) return 0;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  if (hipStreamGetCaptureInfo(st, &cs, &id) != hipSuccess || cs != hipStreamCaptureStatusNone) return 0;
+  const char* off = getenv("FQKV_XCD_LOCAL_MERGE");
+  int res = -1;
+  uint32_t* ids = nullptr;
+  static thread_local uint32_t host[XCC_PROBE_BLOCKS];
+  if (!(off && off[0] == '0') && hipGetSymbolAddress((void**)&ids, HIP_SYMBOL(g_xcc_ids)) == hipSuccess) {
+    hipLaunchKernelGGL(xcc_record_kernel, dim3(XCC_PROBE_BLOCKS), dim3(64), 0, st, ids);
+    if (hipGetLastError() == hipSuccess &&
+        hipMemcpyAsync(host, ids, sizeof(host), hipMemcpyDeviceToHost, st) == hipSuccess &&
+        hipStreamSynchronize(st) == hipSuccess) {
+      uint32_t mx = 0;
+      for (int i = 0; i < XCC_PROBE_BLOCKS; ++i) mx = host[i] > mx ? host[i] : mx;
+      const int n = (int)mx + 1;
+      bool ok = n >= 2;
+      for (int i = 1; ok && i < n; ++i)
+        for (int j = 0; j < i; ++j) ok = ok && host[i] != host[j];
+      for (int i = n; ok && i < XCC_PROBE_BLOCKS; ++i) ok = host[i] == host[i % n];
+      res = ok ? n : -1;
+    }
+  }
+  g_xcd_period[dev].store(res, std::memory_order_release);
+  return res > 0 ? res : 0;
+}
+
 static std::atomic<int> g_pv_valu{0};
 void set_pv_valu(int on) { g_pv_valu.store(on ? 1 : 0, std::memory_order_relaxed); }
 
@@ -1299,6 +1374,13 @@ hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, i
   PartialParams p = params;
   p.split_major = p.S >= 16;
   p.blk_d = p.split_major ? nblocks / p.S : p.S;
+  // the splits of group g are blockIdx.x = s * nwsg + g: one XCD for all of
+  // them when nwsg is a multiple of the XCD period
+  p.xcd_local = 0;
+  if (!p.direct && p.slot >= 0 && p.split_major) {
+    const int n = xcd_period(st);
+    p.xcd_local = n > 0 && (nblocks / p.S) % n == 0;
+  }
   // head grouping: token-major rows (head stride = row bytes), one
   // query-head group per KV row; the heads sharing a 128-byte line of a token
   // (rows under 128 bytes: int4, and int8 at D 64), as many as divide the

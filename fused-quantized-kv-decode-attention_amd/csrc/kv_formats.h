@@ -91,6 +91,7 @@ __device__ __forceinline__ void i4x8_to_h2x4(uint32_t w, h2_t (&h)[4]) {
 // Raw buffer access (gfx9 descriptor word 3 = 0x00020000, stride 0):
 // loads whose byte offset is at or past num_records return zeros.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int CPOL_SC0 = 1;   // cache-policy bit: bypass the CU's L1 (coherent within one XCD's L2)
 constexpr int CPOL_SC1 = 16;  // cache-policy bit: device-scope coherent access
 constexpr int CPOL_NT = 2;    // cache-policy bit: non-temporal (streaming) access
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {

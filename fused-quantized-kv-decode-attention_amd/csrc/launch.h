@@ -54,6 +54,7 @@ struct PartialParams {
   float scale;           // softmax scale (natural-log units for m_part)
   int direct;            // 1: S == 1, write normalised fp16 output
   int slot;              // !direct: arrival-counter slot for the in-kernel merge, -1 = none
+  int xcd_local;         // set by launch_partial: every split of a group runs on one XCD
   // KV layout: row r = (b, h) = (r / hkv, r % hkv) starts at K + b*kv_bs + h*kv_hs
   // and its tokens are kv_ts bytes apart; scales likewise in elements. Paged
   // (page_table != null): b indexes page_table [B, max_pages] and seq_lens [B];

@@ -179,3 +179,43 @@ def test_single_block_workspace_followed_by_nan(merge_mode):
     assert np.isfinite(out).all()
     ref = oracle.gqa_attention(q.numpy(), K.numpy(), V.numpy())
     assert float(np.abs(out.astype(np.float64) - ref).max()) <= TOL
+
+
+@pytest.mark.parametrize("Hkv,N,D,S", [(8, 16384, 128, 32), (8, 512, 128, 16), (64, 4096, 128, 16),
+                                       (8, 8192, 64, 32), (4, 2048, 128, 16)])
+def test_xcd_local_merge_alternating_inputs(Hkv, N, D, S):
+    """With 16 or more splits and a multiple of 8 (KV row, head group) pairs,
+    every split of a group runs on one XCD and the merge meets in that XCD's
+    L2 (8 and 64 groups here); 4 groups keep the device-scope protocol. Two
+    inputs alternate through one scratch buffer six times: each output equals
+    its first result bit for bit (a merge reading the other input's stale
+    partials would not), the partials equal the two-kernel merge's bit for bit,
+    and the output agrees with the oracle."""
+    g = torch.Generator().manual_seed(Hkv * 1000 + N + S)
+    Hq = 4 * Hkv
+    a = make_call(g, Hq=Hq, Hkv=Hkv, N=N, D=D, S=S)
+    b = make_call(g, Hq=Hq, Hkv=Hkv, N=N, D=D, S=S)
+    scratch, o = a[3], a[4]
+    b = b[:3] + (scratch, o, S)
+    first = {}
+    for i in range(12):
+        c = (a, b)[i % 2]
+        run(c)
+        torch.cuda.synchronize()
+        if i < 2:
+            first[i] = (o.clone(), scratch[2].clone())
+        else:
+            assert torch.equal(o, first[i % 2][0]), f"call {i}"
+    fq._ext._set_two_kernel_merge(True)
+    try:
+        for i in (0, 1):
+            run((a, b)[i])
+            torch.cuda.synchronize()
+            assert torch.equal(scratch[2], first[i][1]), f"partials of input {i}"
+    finally:
+        fq._ext._set_two_kernel_merge(False)
+    for i, c in enumerate((a, b)):
+        q, K, V = (x.cpu().double().numpy() for x in c[:3])
+        ref = oracle.gqa_attention(q[None], K[None], V[None])[0]
+        err = np.abs(first[i][0].cpu().double().numpy() - ref).max()
+        assert err <= TOL, (i, err)
