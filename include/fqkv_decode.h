@@ -350,6 +350,15 @@ int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, co
  * kernel then a separate combine kernel, as the reference launches them
  * (decode_attn_gqa_sk_fast.cu:100-111). Results agree to fp32 rounding.
  * Process-wide; returns FQKV_OK.
+ *
+ * The first eager split call on a device (not one on a capturing stream)
+ * launches a small probe on its stream and waits for it, once per process
+ * and device: it records which XCD runs each workgroup. When every split of a
+ * head group runs on one XCD (16 or more splits, head groups a multiple of
+ * the XCD count), the one-kernel merge keeps its partials and counters in
+ * that XCD's L2 instead of device-scope memory; results are bit for bit the
+ * same. FQKV_XCD_LOCAL_MERGE=0 in the environment skips the probe and keeps
+ * the device-scope protocol.
  */
 int fqkv_set_two_kernel_merge(int enable);
 
