@@ -24,10 +24,12 @@
 //      the per-token V scale for int8/int4), as fp16 pairs hi + lo, are then
 //      already in operand-B layout of
 //   4. O^T += V^T P^T with D/16 v_mfma_f32_16x16x32_f16 per pair of tiles,
-//      after a 4 x 4 exchange of the V chunks between lane rows and
-//      registers (v_permlane32_swap / v_permlane16_swap) puts four tokens of
-//      one head-dim element in each operand slot; int8/int4 become exact
-//      fp16 on the way. Each tile's weights enter operand B in the columns
+//      with four tokens of one head-dim element in each operand slot: fp16 /
+//      bf16 lanes load their own four tokens' row segments; narrower rows
+//      load four consecutive rows per instruction and a 4 x 4 exchange of
+//      the V chunks between lane rows and registers (v_permlane32_swap /
+//      v_permlane16_swap) regroups them; int8/int4 become exact fp16 on the
+//      way. Each tile's weights enter operand B in the columns
 //      0 .. HG-1 that are emitted (fp16: moved there by a DPP row shift) or
 //      in the tile's own columns, the rest zero, summed at the end (int8 /
 //      int4, whose products carry a bias until then).
@@ -66,7 +68,8 @@ constexpr float LOG2E = 1.4426950408889634f;
 
 // Timeline instrumentation, compiled in only with -DFQKV_TIMELINE: lane 0 of
 // each wave records the 100 MHz real-time counter at the kernel's stages into
-// g_timeline[workgroup][wave][stage] (for a host-side harness to read back).
+// g_timeline[workgroup][wave][stage], which fqkv_timeline_read copies to the
+// host (or, with bytes = SIZE_MAX, clears).
 #ifdef FQKV_TIMELINE
 constexpr int TIMELINE_BLOCKS = 4096;
 __device__ unsigned long long g_timeline[TIMELINE_BLOCKS][NW_MAX][16];
@@ -75,6 +78,13 @@ __device__ unsigned long long g_timeline[TIMELINE_BLOCKS][NW_MAX][16];
     if ((threadIdx.x & 63) == 0 && blockIdx.x < TIMELINE_BLOCKS)                                   \
       g_timeline[blockIdx.x][threadIdx.x >> 6][stage] = __builtin_amdgcn_s_memrealtime();          \
   } while (0)
+extern "C" int fqkv_timeline_read(void* host, size_t bytes) {
+  if (bytes == (size_t)-1) {
+    static unsigned long long z[TIMELINE_BLOCKS][NW_MAX][16];
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(g_timeline), z, sizeof(z));
+  }
+  return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(g_timeline), bytes);
+}
 #else
 #define FQKV_STAMP(stage) \
   do {                    \
@@ -369,6 +379,7 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
 #pragma unroll
       for (int j = 0; j < NJ; ++j) ov[j] = ld4(rO, (uint32_t)((4 * j + kr) * D * 4) + qo);  // zero past split S - 1
       float M = wave_max(lane < S ? m0 : -INFINITY);
+      FQKV_STAMP(8);  // merge: maximum over the splits known
       if (M == -INFINITY) M = 0.0f;  // every split empty: all weights 0
       const float w = lane < S ? fast_exp2((m0 - M) * LOG2E) : 0.0f;
       s_w[wv][lane] = w;
@@ -502,26 +513,36 @@ template <int D, int HG, int NWC>
 __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const float (*s_o)[HG][opitch<D>()],
                                                  const float (*s_m)[NW_MAX], const float (*s_l)[NW_MAX],
                                                  size_t qrow0, int hcnt, int s) {
+  const int lane = threadIdx.x & 63;
   for (int idx = threadIdx.x; idx < hcnt * D; idx += blockDim.x) {
     const int h = __builtin_amdgcn_readfirstlane(idx / D);
     const int d = idx % D;
-    float mw[NWC], lw[NWC], ow[NWC];
-#pragma unroll
-    for (int ww = 0; ww < NWC; ++ww) {
-      mw[ww] = s_m[h][ww];
-      lw[ww] = s_l[h][ww];
-      ow[ww] = s_o[ww][h][d];
+    // the head's wave weights once per wave: lane j < NWC holds wave j's (m, l)
+    const float mj = lane < NWC ? s_m[h][lane & (NWC - 1)] : -INFINITY;
+    const float lj = lane < NWC ? s_l[h][lane & (NWC - 1)] : 0.0f;
+    int k = fkey(mj);
+    k = max(k, dpp_i<0xB1>(k));
+    k = max(k, dpp_i<0x4E>(k));
+    if constexpr (NWC > 4) {  // fold the row's four quads (rotations by 4 and 8 lanes)
+      k = max(k, dpp_i<0x124>(k));
+      k = max(k, dpp_i<0x128>(k));
     }
-    float M = mw[0];
-#pragma unroll
-    for (int ww = 1; ww < NWC; ++ww) M = fmaxf(M, mw[ww]);
+    const float M = unkey(__builtin_amdgcn_readlane(k, 0));
     const float Mu = (M == -INFINITY) ? 0.0f : M;
-    float L = 0.0f, O = 0.0f;
+    const float wj = lane < NWC ? fast_exp2((mj - Mu) * p.c) : 0.0f;
+    float lw = wj * lj;
+    lw += dpp_f<0xB1>(lw);
+    lw += dpp_f<0x4E>(lw);
+    if constexpr (NWC > 4) {
+      lw += dpp_f<0x124>(lw);
+      lw += dpp_f<0x128>(lw);
+    }
+    const float L = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lw), 0));
+    float O = 0.0f;
 #pragma unroll
     for (int ww = 0; ww < NWC; ++ww) {
-      const float sc = fast_exp2((mw[ww] - Mu) * p.c);
-      L = fmaf(sc, lw[ww], L);
-      O = fmaf(sc, ow[ww], O);
+      const float sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), ww));
+      O = fmaf(sc, s_o[ww][h][d], O);
     }
     const size_t qh = qrow0 + h;
     if (p.direct) {
@@ -553,6 +574,33 @@ __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const f
       // output too and no merge follows (one launch per call)
       if (p.S == 1) p.o[qh * D + d] = L > 0.0f ? (_Float16)(O / L) : (_Float16)0.0f;
     }
+  }
+}
+
+// Forces the launch constants into scalar registers at this point (an empty
+// asm that reads them), so the compiler issues their kernel-argument loads as
+// one batch instead of next to each first use.
+template <typename T>
+__device__ __forceinline__ void pin_s(T v) {
+  asm volatile("" ::"s"(v));
+}
+template <bool QUANT, bool PAGED>
+__device__ __forceinline__ void pin_sgprs(const PartialParams& p) {
+  pin_s(p.q); pin_s(p.K); pin_s(p.V);
+  pin_s(p.G); pin_s(p.N); pin_s(p.chunk); pin_s(p.ngroups); pin_s(p.c);
+  pin_s(p.hkv); pin_s(p.kv_hs); pin_s(p.kv_ts);
+  pin_s(p.split_major); pin_s(p.blk_d);
+  pin_s(p.div_blk.magic); pin_s(p.div_blk.shift); pin_s(p.div_groups.magic); pin_s(p.div_groups.shift);
+  pin_s(p.div_hkv.magic); pin_s(p.div_hkv.shift); pin_s(p.hg_k); pin_s(p.hg_d);
+  if constexpr (!PAGED) pin_s(p.kv_bs);
+  if constexpr (QUANT) {
+    pin_s(p.Ks); pin_s(p.Vs); pin_s(p.sc_hs); pin_s(p.sc_ts);
+    if constexpr (!PAGED) pin_s(p.sc_bs);
+  }
+  if constexpr (PAGED) {
+    pin_s(p.kv_bs); pin_s(p.page_table); pin_s(p.seq_lens); pin_s(p.max_pages); pin_s(p.page_log2);
+    pin_s(p.num_pages);
+    if constexpr (QUANT) pin_s(p.sc_bs);
   }
 }
 
@@ -601,13 +649,19 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   const int nw = blockDim.x >> 6;
   // blockIdx.x = s * nwsg + wsg or wsg * S + s (wsg = r * ngroups + hg),
   // decomposed with multiply-shift divisions
+  // Every launch constant in one scalar-load round trip: read here, in the
+  // entry block, so the loads leave together (lazily placed, they took four
+  // dependent round trips before the first KV load, and one more before the
+  // epilogue).
+  pin_sgprs<F::QUANT, PAGED>(p);
   const uint32_t bq = fast_div(blockIdx.x, p.div_blk);
   const uint32_t br = blockIdx.x - bq * (uint32_t)p.blk_d;
   uint32_t wsg = p.split_major ? br : bq;
   const int s = (int)(p.split_major ? bq : br);
-  if (p.hg_k) {
+  {
     // in a block of 2^(hg_k + hg_d) groups, group e 2^hg_d + c becomes row c 2^hg_k + e:
-    // head e of head set c, the set's heads 2^hg_d groups apart
+    // head e of head set c, the set's heads 2^hg_d groups apart (the identity
+    // when hg_k = hg_d = 0; no branch, so the prologue stays one block)
     const uint32_t k = (uint32_t)p.hg_k, d = (uint32_t)p.hg_d;
     const uint32_t low = wsg & ((1u << (k + d)) - 1u);
     wsg = (wsg - low) | ((low & ((1u << d) - 1u)) << k) | (low >> d);
@@ -716,7 +770,11 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     koff = F::krow_lane(lane, ts);
   else
     koff = (uint32_t)n * ts + F::klane(R);
-  const uint32_t voff = (uint32_t)R * ts + (uint32_t)n * VG::VBYTES;
+  // 2-byte rows (fp16, bf16): lane row R loads tokens 4R .. 4R+3 itself (load j
+  // = token 4R + j), each load still whole row segments; narrower rows load
+  // token 4j + R and trade chunks between lane rows afterwards (exchange_4x4)
+  constexpr bool VDIRECT = FMT == KV_F16 || FMT == KV_BF16;
+  const uint32_t voff = (uint32_t)(VDIRECT ? 4 * R : R) * ts + (uint32_t)n * VG::VBYTES;
   // tile t's sources: descriptors and the byte offset of its first token
   struct TileSrc {
     rsrc_t k, v, ks, vs;
@@ -849,10 +907,11 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     for (int u = 0; u < U; ++u) {
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        load_vchunk<VG::VBYTES, VD, VCP>(src[u].v, voff + (uint32_t)(4 * j) * ts + (F::SOFF_TILE ? 0u : src[u].off),
+        load_vchunk<VG::VBYTES, VD, VCP>(src[u].v, voff + (uint32_t)(VDIRECT ? j : 4 * j) * ts + (F::SOFF_TILE ? 0u : src[u].off),
                                          vr[u][j], F::SOFF_TILE ? src[u].off : 0u);
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
+    FQKV_STAMP(1);  // every load of the pass issued
 
     if constexpr (PICK_SC) {
 #pragma unroll
@@ -1016,8 +1075,10 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       // head are one LDS broadcast read per row
 #pragma unroll
       for (int u = 0; u < U; ++u) {
+        if constexpr (!VDIRECT) {
 #pragma unroll
-        for (int dw = 0; dw < VD; ++dw) exchange_4x4(vr[u][0][dw], vr[u][1][dw], vr[u][2][dw], vr[u][3][dw]);
+          for (int dw = 0; dw < VD; ++dw) exchange_4x4(vr[u][0][dw], vr[u][1][dw], vr[u][2][dw], vr[u][3][dw]);
+        }
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           float wt[HG];
@@ -1052,7 +1113,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       auto wts = [&](int t, h4_t& bh, h4_t& bl) {
 #pragma unroll
         for (int dw = 0; dw < VD; ++dw) {
-          exchange_4x4(vr[t][0][dw], vr[t][1][dw], vr[t][2][dw], vr[t][3][dw]);
+          if constexpr (!VDIRECT) exchange_4x4(vr[t][0][dw], vr[t][1][dw], vr[t][2][dw], vr[t][3][dw]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) vr[t][j][dw] = F::vprep(vr[t][j][dw]);
         }
