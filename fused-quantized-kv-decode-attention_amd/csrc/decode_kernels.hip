@@ -356,11 +356,16 @@ __device__ __forceinline__ void merge_splits(const float* __restrict__ m_part, c
     unit[i] = L > 0.0f ? (_Float16)(v / L) : (_Float16)0.0f;
   };
   auto emit = [&](fl4_t a, float L, _Float16* dst) {
-    a.x = rows4_sum(a.x);
-    a.y = rows4_sum(a.y);
-    a.z = rows4_sum(a.z);
-    a.w = rows4_sum(a.w);
-    const float v = kr == 0 ? a.x : (kr == 1 ? a.y : (kr == 2 ? a.z : a.w));
+    // lane row kr needs component kr summed over the four lane rows: after a
+    // 4 x 4 exchange, register j of row kr holds component kr of row j
+    // (components copied to scalars first: a bit cast of a vector-element
+    // expression reads element 0 with this compiler, whatever the index)
+    const float ax = a.x, ay = a.y, az = a.z, aw = a.w;
+    uint32_t a0 = __builtin_bit_cast(uint32_t, ax), a1 = __builtin_bit_cast(uint32_t, ay),
+             a2 = __builtin_bit_cast(uint32_t, az), a3 = __builtin_bit_cast(uint32_t, aw);
+    exchange_4x4(a0, a1, a2, a3);
+    const float v = (__builtin_bit_cast(float, a0) + __builtin_bit_cast(float, a2)) +
+                    (__builtin_bit_cast(float, a1) + __builtin_bit_cast(float, a3));
     put(dst, 4 * (lane & 15) + kr, v, L);
   };
   if (S <= CHK && units <= nw) {
