@@ -49,8 +49,8 @@ constexpr int MAX_DEV = 64;
 // that never run at the same time, because the kernel of a call leaves its
 // counters at zero only when it ends. Calls on one stream run in order, so
 // each stream keeps one slot for its eager calls (EAGER_SLOTS of them, first
-// come first served), and each stream capture takes a slot of its own that
-// eager calls never use (the captured graph replays that slot, so two
+// come first served), and each stream of a capture takes a slot of its own
+// that eager calls never use (the captured graph replays that slot, so two
 // replays of one graph must not overlap -- they would share the caller's
 // scratch and output too). Streams or captures beyond the free slots, and the
 // per-thread default stream (one handle for many streams), get the
@@ -60,14 +60,51 @@ std::atomic<int> g_force_two_kernel{0};
 // per batch size keeps the one-kernel merge in every graph); 64 KiB of counters each
 constexpr int EAGER_SLOTS = 12;
 
+// A slot's stream: its slot, and whether its workgroups may use the XCD-local
+// merge (a stream created with a CU mask that leaves CUs out may deal
+// workgroups to XCDs in another order, so it keeps the device-scope merge).
+struct SlotEntry {
+  hipStream_t stream;
+  unsigned long long capture;  // capture id (captured slots)
+  int slot;
+  int xcd_ok;
+};
 struct SlotTable {
   std::mutex mu;
-  std::vector<std::pair<hipStream_t, int>> eager;
-  std::vector<std::pair<unsigned long long, int>> captured;
+  std::vector<SlotEntry> eager;
+  std::vector<SlotEntry> captured;
 };
 SlotTable g_slot_tables[MAX_DEV];
 
-int merge_slot(hipStream_t st, int64_t groups) {
+// Calls that wanted the in-kernel merge but found every slot of their kind
+// taken, and so took the two-kernel merge.
+std::atomic<int64_t> g_slot_fallbacks{0};
+// The merge protocol of the calling thread's last call (FQKV_MERGE_*).
+thread_local int g_last_protocol = FQKV_MERGE_NONE;
+
+// 1 when the stream's CU mask (hipExtStreamGetCUMask) covers as many CUs as
+// the device has, 0 when it leaves some out or cannot be read. The null
+// stream has no CU mask of its own.
+int stream_full_cu_mask(hipStream_t st, int dev) {
+  if (st == nullptr) return 1;
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) return 0;
+  uint32_t mask[32] = {};
+  const uint32_t words = (uint32_t)((cus + 31) / 32);
+  if (words > 32 || hipExtStreamGetCUMask(st, words, mask) != hipSuccess) return 0;
+  int set = 0;
+  for (uint32_t i = 0; i < words; ++i) set += __builtin_popcount(mask[i]);
+  return set >= cus;
+}
+
+// Slot of a call with `groups` (KV row, head group) pairs on stream st, or -1
+// (two-kernel merge); *xcd_ok receives whether the stream may take the
+// XCD-local merge. Eager slots are keyed by stream, captured ones by (capture
+// id, stream): streams that joined one capture through event waits report the
+// same capture id, and their nodes may run side by side on replay, while the
+// nodes captured from one stream are ordered.
+int merge_slot(hipStream_t st, int64_t groups, int* xcd_ok) {
+  *xcd_ok = 0;
   if (g_force_two_kernel.load(std::memory_order_relaxed) || groups > MAX_SPLIT_GROUPS) return -1;
   if (st == hipStreamPerThread) return -1;
   int dev = 0;
@@ -76,23 +113,31 @@ int merge_slot(hipStream_t st, int64_t groups) {
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   unsigned long long id = 0;
   if (hipStreamGetCaptureInfo(st, &cs, &id) != hipSuccess) return -1;
+  if (cs != hipStreamCaptureStatusNone && cs != hipStreamCaptureStatusActive)
+    return -1;  // invalidated capture: the launch fails anyway
   SlotTable& t = g_slot_tables[dev];
   std::lock_guard<std::mutex> lock(t.mu);
-  if (cs == hipStreamCaptureStatusActive) {
-    for (const auto& e : t.captured)
-      if (e.first == id) return e.second;
-    if ((int)t.captured.size() >= SPLIT_SLOTS - EAGER_SLOTS) return -1;
-    const int slot = EAGER_SLOTS + (int)t.captured.size();
-    t.captured.emplace_back(id, slot);
-    return slot;
+  const bool cap = cs == hipStreamCaptureStatusActive;
+  std::vector<SlotEntry>& v = cap ? t.captured : t.eager;
+  for (const auto& e : v)
+    if (e.stream == st && (!cap || e.capture == id)) {
+      *xcd_ok = e.xcd_ok;
+      return e.slot;
+    }
+  if ((int)v.size() >= (cap ? SPLIT_SLOTS - EAGER_SLOTS : EAGER_SLOTS)) {
+    g_slot_fallbacks.fetch_add(1, std::memory_order_relaxed);
+    return -1;
   }
-  if (cs != hipStreamCaptureStatusNone) return -1;  // invalidated capture: the launch fails anyway
-  for (const auto& e : t.eager)
-    if (e.first == st) return e.second;
-  if ((int)t.eager.size() >= EAGER_SLOTS) return -1;
-  const int slot = (int)t.eager.size();
-  t.eager.emplace_back(st, slot);
-  return slot;
+  SlotEntry e{st, cap ? id : 0ull, (cap ? EAGER_SLOTS : 0) + (int)v.size(), stream_full_cu_mask(st, dev)};
+  v.push_back(e);
+  *xcd_ok = e.xcd_ok;
+  return e.slot;
+}
+
+int record_protocol(int S, int slot, int xcd_local) {
+  g_last_protocol = S <= 1 ? FQKV_MERGE_NONE
+                           : (slot < 0 ? FQKV_MERGE_TWO_KERNEL : (xcd_local ? FQKV_MERGE_XCD_LOCAL : FQKV_MERGE_DEVICE));
+  return g_last_protocol;
 }
 
 // CU count per device, queried once (256 on MI355X).
@@ -229,15 +274,17 @@ int run_decode(int fmt, const void* q, const void* K, const void* V, const void*
     p.m_part = f;
     p.l_part = f + heads * S;
     p.o_part = f + acc_offset_floats(heads, S);
-    p.slot = merge_slot(st, rows * ngroups);
+    p.slot = merge_slot(st, rows * ngroups, &p.xcd_ok);
   }
   // With four or more work items per CU, workgroups of 4 waves: several
   // share a CU and hide each other's memory latency (measured on MI355X, MHA
   // at N 4096: never slower than 8 waves from batch 1024 on, 5-12 % faster
   // for int4 / int8 at D 128 and fp16 at D 64). W is a maximum.
   const int64_t nw = (nblocks >= 4LL * cus && W > 4) ? 4 : W;
-  hipError_t e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)nw, st);
+  int xcd_local = 0;
+  hipError_t e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)nw, st, &xcd_local);
   if (e != hipSuccess) return hip_fail(e, "launch: partial kernel");
+  record_protocol((int)S, p.slot, xcd_local);
   if (!p.direct && p.slot < 0) {
     e = launch_combine((int)D, p.m_part, p.l_part, p.o_part, o, (int)heads, (int)S, 4, st);
     if (e != hipSuccess) return hip_fail(e, "launch: combine kernel");
@@ -327,11 +374,13 @@ int sk_fast(int fmt, const void* q, const void* K, const void* V, const void* Ks
   set_contiguous_layout(p, Hkv, N, (int)row_bytes_of(fmt, D));
   // S == 1 still writes the scratch (the caller asked for it); with one split
   // the partial kernel also writes the output, and no merge is launched.
-  p.slot = S > 1 ? merge_slot(st, Hkv * ngroups) : -1;
+  p.slot = S > 1 ? merge_slot(st, Hkv * ngroups, &p.xcd_ok) : -1;
   hipError_t e;
   if (ev_begin && (e = hipEventRecord((hipEvent_t)ev_begin, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
-  e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)W, st);
+  int xcd_local = 0;
+  e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)W, st, &xcd_local);
   if (e != hipSuccess) return hip_fail(e, "partial");
+  record_protocol((int)S, p.slot, xcd_local);
   if (ev_end && (e = hipEventRecord((hipEvent_t)ev_end, st)) != hipSuccess) return hip_fail(e, "hipEventRecord");
   if (S > 1 && p.slot < 0) {
     e = launch_combine((int)D, m_part, l_part, o_part, o, (int)Hq, (int)S, (int)CW, st);
@@ -397,6 +446,23 @@ int fqkv_set_pv_valu(int enable) {
 
 int fqkv_set_two_kernel_merge(int enable) {
   g_force_two_kernel.store(enable ? 1 : 0, std::memory_order_relaxed);
+  return FQKV_OK;
+}
+
+int fqkv_last_merge_protocol(void) { return g_last_protocol; }
+
+int64_t fqkv_merge_fallback_count(void) { return g_slot_fallbacks.load(std::memory_order_relaxed); }
+
+int fqkv_xcd_period(int device) { return xcd_period_of(device); }
+
+int fqkv_release_capture_slots(void) {
+  int dev = 0;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= MAX_DEV) return fail(FQKV_ERR_HIP, "device index %d out of range", dev);
+  SlotTable& t = g_slot_tables[dev];
+  std::lock_guard<std::mutex> lock(t.mu);
+  t.captured.clear();
   return FQKV_OK;
 }
 

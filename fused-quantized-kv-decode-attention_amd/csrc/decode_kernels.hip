@@ -57,6 +57,7 @@
 #include <stdlib.h>
 
 #include <atomic>
+#include <mutex>
 #include <numeric>
 
 #include "kv_formats.h"
@@ -1335,54 +1336,87 @@ __global__ void dequant_kernel(const uint8_t* __restrict__ Kq, const _Float16* _
 // ------------------------------------------------------------ launchers ----
 // XCD period of a device: the workgroups of a launch are dealt to the XCDs
 // round-robin by blockIdx.x. A one-time probe records every workgroup's XCC_ID
-// (hardware register 20, bits 3:0) over 4096 workgroups and accepts n >= 2
-// only if the first n workgroups sit on n distinct XCDs and workgroup i on the
-// XCD of workgroup i mod n; otherwise (a register that reads one value, any
-// other order) the split merge keeps its device-scope protocol.
+// (hardware register 20, bits 3:0) over 4096 workgroups; with n the number of
+// distinct ids it accepts n >= 2 only if workgroup i sits on the XCD of
+// workgroup i mod n (so the first n are on n distinct XCDs); otherwise (a
+// register that reads one value, any other order) the split merge keeps its
+// device-scope protocol.
 constexpr int XCC_PROBE_BLOCKS = 4096;
 constexpr int XCC_ID_HWREG = (3 << 11) | 20;  // s_getreg operand: 4 bits at offset 0 of register 20
 static __device__ __align__(256) uint32_t g_xcc_ids[XCC_PROBE_BLOCKS];
 static std::atomic<int> g_xcd_period[64];  // 0: not probed, -1: not usable, n: period
+static std::mutex g_xcd_probe_mu[64];
 
 __global__ void __launch_bounds__(64) xcc_record_kernel(uint32_t* ids) {
   if (threadIdx.x == 0) ids[blockIdx.x] = (uint32_t)__builtin_amdgcn_s_getreg(XCC_ID_HWREG) & 15u;
 }
 
-// Probed on the first eager call per device (a stream that is capturing gets
-// 0, the device-scope protocol, and leaves the probe for later); reads the
-// 16 KiB of ids back on the caller's stream. Allocates nothing.
+// The period a run of ids shows: n distinct ids repeating with period n, or
+// -1 (one id, or any other order).
+static int period_of_ids(const uint32_t* ids, int count) {
+  bool seen[16] = {};
+  int n = 0;
+  for (int i = 0; i < count; ++i)
+    if (!seen[ids[i] & 15u]) {
+      seen[ids[i] & 15u] = true;
+      ++n;
+    }
+  if (n < 2) return -1;
+  for (int i = 1; i < n; ++i)
+    for (int j = 0; j < i; ++j)
+      if (ids[i] == ids[j]) return -1;
+  for (int i = n; i < count; ++i)
+    if (ids[i] != ids[i % n]) return -1;
+  return n;
+}
+
+// Probed on the first eager call per device, one thread at a time (a stream
+// that is capturing gets 0, the device-scope protocol, and leaves the probe
+// for later). It launches the probe kernel and reads the 16 KiB of ids back
+// on the caller's stream, so that first call synchronises the stream once;
+// the synchronisation runs in this thread's relaxed capture mode, so a stream
+// capture in progress on another thread is not invalidated by it. A HIP error
+// stores nothing (a later call probes again); FQKV_XCD_LOCAL_MERGE=0 in the
+// environment stores -1. Allocates nothing.
 static int xcd_period(hipStream_t st) {
   int dev = 0, cur = 0;
   if ((st ? hipStreamGetDevice(st, &dev) : hipGetDevice(&dev)) != hipSuccess || hipGetDevice(&cur) != hipSuccess ||
       dev != cur || dev < 0 || dev >= 64)
     return 0;
-  const int known = g_xcd_period[dev].load(std::memory_order_acquire);
+  int known = g_xcd_period[dev].load(std::memory_order_acquire);
   if (known != 0) return known > 0 ? known : 0;
   if (st == hipStreamPerThread) return 0;
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   unsigned long long id = 0;
   if (hipStreamGetCaptureInfo(st, &cs, &id) != hipSuccess || cs != hipStreamCaptureStatusNone) return 0;
+  std::lock_guard<std::mutex> lock(g_xcd_probe_mu[dev]);
+  known = g_xcd_period[dev].load(std::memory_order_acquire);
+  if (known != 0) return known > 0 ? known : 0;
   const char* off = getenv("FQKV_XCD_LOCAL_MERGE");
-  int res = -1;
-  uint32_t* ids = nullptr;
-  static thread_local uint32_t host[XCC_PROBE_BLOCKS];
-  if (!(off && off[0] == '0') && hipGetSymbolAddress((void**)&ids, HIP_SYMBOL(g_xcc_ids)) == hipSuccess) {
-    hipLaunchKernelGGL(xcc_record_kernel, dim3(XCC_PROBE_BLOCKS), dim3(64), 0, st, ids);
-    if (hipGetLastError() == hipSuccess &&
-        hipMemcpyAsync(host, ids, sizeof(host), hipMemcpyDeviceToHost, st) == hipSuccess &&
-        hipStreamSynchronize(st) == hipSuccess) {
-      uint32_t mx = 0;
-      for (int i = 0; i < XCC_PROBE_BLOCKS; ++i) mx = host[i] > mx ? host[i] : mx;
-      const int n = (int)mx + 1;
-      bool ok = n >= 2;
-      for (int i = 1; ok && i < n; ++i)
-        for (int j = 0; j < i; ++j) ok = ok && host[i] != host[j];
-      for (int i = n; ok && i < XCC_PROBE_BLOCKS; ++i) ok = host[i] == host[i % n];
-      res = ok ? n : -1;
-    }
+  if (off && off[0] == '0') {
+    g_xcd_period[dev].store(-1, std::memory_order_release);
+    return 0;
   }
+  uint32_t* ids = nullptr;
+  static uint32_t host[64][XCC_PROBE_BLOCKS];  // guarded by the device's probe mutex
+  if (hipGetSymbolAddress((void**)&ids, HIP_SYMBOL(g_xcc_ids)) != hipSuccess) return 0;
+  void* args[] = {&ids};
+  if (hipLaunchKernel((const void*)xcc_record_kernel, dim3(XCC_PROBE_BLOCKS), dim3(64), args, 0, st) != hipSuccess)
+    return 0;
+  hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+  if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return 0;
+  const bool copied = hipMemcpyAsync(host[dev], ids, sizeof(host[dev]), hipMemcpyDeviceToHost, st) == hipSuccess &&
+                      hipStreamSynchronize(st) == hipSuccess;
+  (void)hipThreadExchangeStreamCaptureMode(&mode);  // restores the caller's mode
+  if (!copied) return 0;
+  const int res = period_of_ids(host[dev], XCC_PROBE_BLOCKS);
   g_xcd_period[dev].store(res, std::memory_order_release);
   return res > 0 ? res : 0;
+}
+
+int xcd_period_of(int device) {
+  if (device < 0 || device >= 64) return -1;
+  return g_xcd_period[device].load(std::memory_order_acquire);
 }
 
 static std::atomic<int> g_pv_valu{0};
@@ -1433,7 +1467,7 @@ static hipError_t launch_partial_d(int hg, const PartialParams& p, int nblocks, 
 }
 
 hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, int nblocks, int nw,
-                          hipStream_t st) {
+                          hipStream_t st, int* xcd_local) {
   if ((nw != 2 && nw != 4 && nw != 8) || nblocks < 1 || params.S < 1 || params.ngroups < 1 || params.hkv < 1 ||
       nblocks % params.S != 0)
     return hipErrorInvalidValue;
@@ -1443,10 +1477,11 @@ hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& params, i
   // the splits of group g are blockIdx.x = s * nwsg + g: one XCD for all of
   // them when nwsg is a multiple of the XCD period
   p.xcd_local = 0;
-  if (!p.direct && p.slot >= 0 && p.split_major) {
+  if (!p.direct && p.slot >= 0 && p.split_major && p.xcd_ok) {
     const int n = xcd_period(st);
     p.xcd_local = n > 0 && (nblocks / p.S) % n == 0;
   }
+  if (xcd_local) *xcd_local = p.xcd_local;
   // head grouping: token-major rows (head stride = row bytes), one
   // query-head group per KV row; the heads sharing a 128-byte line of a token
   // (rows under 128 bytes: int4, and int8 at D 64), as many as divide the

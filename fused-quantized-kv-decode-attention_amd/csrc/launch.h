@@ -54,6 +54,7 @@ struct PartialParams {
   float scale;           // softmax scale (natural-log units for m_part)
   int direct;            // 1: S == 1, write normalised fp16 output
   int slot;              // !direct: arrival-counter slot for the in-kernel merge, -1 = none
+  int xcd_ok;            // set by the caller: the stream may take the XCD-local merge (no CU mask)
   int xcd_local;         // set by launch_partial: every split of a group runs on one XCD
   // KV layout: row r = (b, h) = (r / hkv, r % hkv) starts at K + b*kv_bs + h*kv_hs
   // and its tokens are kv_ts bytes apart; scales likewise in elements. Paged
@@ -105,8 +106,14 @@ inline void set_contiguous_layout(PartialParams& p, int64_t rows, int64_t N, int
 constexpr int SPLIT_SLOTS = 128;
 constexpr int MAX_SPLIT_GROUPS = 16384;
 
+// *xcd_local (optional) receives whether the in-kernel split merge of this
+// launch meets in one XCD's L2 (1) or at device scope (0).
 hipError_t launch_partial(int fmt, int D, int hg, const PartialParams& p, int nblocks, int nw,
-                          hipStream_t st);
+                          hipStream_t st, int* xcd_local = nullptr);
+// XCD period of a device as probed (> 0), 0 while not probed (or after a
+// probe that a HIP error cut short: it runs again on a later call), -1 when
+// the probe found no usable round-robin order.
+int xcd_period_of(int device);
 hipError_t launch_combine(int D, const float* m_part, const float* l_part, const float* o_part,
                           void* o, int H, int S, int nw, hipStream_t st);
 hipError_t launch_dequant(int fmt, int D, int path, const void* Kq, const void* Ks, float* out,

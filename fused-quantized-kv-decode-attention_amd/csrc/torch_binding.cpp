@@ -766,4 +766,15 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, m) {
         "measurement knob: P.V on the vector ALUs (fp16, D 128, 1 or 4 heads per group, contiguous rows)");
   m.def("_set_two_kernel_merge", [](bool enable) { fqkv_set_two_kernel_merge(enable ? 1 : 0); },
         "force the two-kernel split merge (testing / comparison)");
+  m.def("_last_merge_protocol", []() { return fqkv_last_merge_protocol(); },
+        "split merge of this thread's last call: 0 none, 1 two-kernel, 2 device scope, 3 XCD-local");
+  m.def("_merge_fallback_count", []() { return fqkv_merge_fallback_count(); },
+        "calls that took the two-kernel merge because no counter slot was free");
+  m.def("_xcd_period", [](int device) { return fqkv_xcd_period(device); },
+        "XCD period the probe found (> 0), 0 before the probe, -1 when unusable");
+  m.def("_release_capture_slots", []() {
+        const int rc = fqkv_release_capture_slots();
+        TORCH_CHECK(rc == FQKV_OK, "release_capture_slots: ", fqkv_last_error());
+      },
+        "free the capture slots of the current device (after destroying every graph that used them)");
 }

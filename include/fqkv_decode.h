@@ -61,6 +61,11 @@ enum {
  * reference. */
 enum { FQKV_KV_F16 = 0, FQKV_KV_I8 = 1, FQKV_KV_I4 = 2, FQKV_KV_BF16 = 3, FQKV_KV_FP8 = 4 };
 
+/* The split merge a call used (fqkv_last_merge_protocol): none (one split),
+ * the two-kernel form, the one-kernel form at device scope, or the one-kernel
+ * form meeting in one XCD's L2. */
+enum { FQKV_MERGE_NONE = 0, FQKV_MERGE_TWO_KERNEL = 1, FQKV_MERGE_DEVICE = 2, FQKV_MERGE_XCD_LOCAL = 3 };
+
 /* element type of a quantizer input; bf16 rows widen exactly to fp32 and are
  * quantized as fp32 (no counterpart in the reference, whose quantizers see
  * fp16 or fp32 tensors) */
@@ -341,26 +346,54 @@ int fqkv_quantize_kv_paged(const void* K_new, const void* V_new, int x_dtype, co
  * one kernel per call; the last workgroup of each head group to finish merges
  * that group's split partials, using library-owned arrival counters. The
  * counters come in 128 slots per device: each stream keeps one of 12 slots for
- * its eager calls (first come, first served), and each stream capture takes
+ * its eager calls (first come, first served), and each stream of each stream
+ * capture (streams that join a capture through event waits each count) takes
  * one of the other 116 for the graph it records; calls on a stream or capture
  * with no free slot, and calls on hipStreamPerThread, use the two-kernel
- * merge. So calls that may overlap never share a slot; the one exception a
- * caller must avoid is replaying one captured graph on two streams at once
- * (those replays also share the caller's scratch and output). 1: a partial
- * kernel then a separate combine kernel, as the reference launches them
- * (decode_attn_gqa_sk_fast.cu:100-111). Results agree to fp32 rounding.
- * Process-wide; returns FQKV_OK.
+ * merge (fqkv_merge_fallback_count counts the calls that found no free slot).
+ * So calls that may overlap never share a slot, with two exceptions a caller
+ * must avoid: replaying one captured graph on two streams at once (those
+ * replays also share the caller's scratch and output), and destroying a
+ * stream with split calls still queued and creating a new one that gets the
+ * same handle before they finish. Capture slots stay taken until
+ * fqkv_release_capture_slots. 1: a partial kernel then a separate combine
+ * kernel, as the reference launches them (decode_attn_gqa_sk_fast.cu:100-111).
+ * Results agree to fp32 rounding. Process-wide; returns FQKV_OK.
  *
  * The first eager split call on a device (not one on a capturing stream)
  * launches a small probe on its stream and waits for it, once per process
  * and device: it records which XCD runs each workgroup. When every split of a
  * head group runs on one XCD (16 or more splits, head groups a multiple of
- * the XCD count), the one-kernel merge keeps its partials and counters in
- * that XCD's L2 instead of device-scope memory; results are bit for bit the
- * same. FQKV_XCD_LOCAL_MERGE=0 in the environment skips the probe and keeps
- * the device-scope protocol.
+ * the XCD count) and the stream has no CU mask that leaves CUs out, the
+ * one-kernel merge keeps its partials and counters in that XCD's L2 instead
+ * of device-scope memory; results are bit for bit the same.
+ * FQKV_XCD_LOCAL_MERGE=0 in the environment skips the probe and keeps the
+ * device-scope protocol.
  */
 int fqkv_set_two_kernel_merge(int enable);
+
+/*
+ * Diagnostics of the split merge (no counterpart in the reference; for tests,
+ * benchmarks and callers checking which path their calls take).
+ * fqkv_last_merge_protocol: the FQKV_MERGE_* protocol of the calling thread's
+ * last successful decode call. fqkv_merge_fallback_count: calls since the
+ * library loaded that took the two-kernel merge because every counter slot of
+ * their kind (eager or captured) was taken. fqkv_xcd_period: the XCD period
+ * the probe found on `device` (> 0), 0 while it has not run, -1 when it found
+ * no usable order (or FQKV_XCD_LOCAL_MERGE=0).
+ */
+int fqkv_last_merge_protocol(void);
+int64_t fqkv_merge_fallback_count(void);
+int fqkv_xcd_period(int device);
+
+/*
+ * Frees every capture slot of the current device, so later captures take
+ * the one-kernel merge again once all 116 have been used. Call it only after
+ * destroying every graph that captured split calls on this device: a graph
+ * replayed afterwards could share its counters with a new capture's. No
+ * counterpart in the reference. Returns FQKV_OK.
+ */
+int fqkv_release_capture_slots(void);
 
 /*
  * Measurement knob: with `enable` nonzero, fp16 calls at D = 128 whose work

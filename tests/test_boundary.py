@@ -58,6 +58,16 @@ def test_version(lib):
     assert b"gfx950" in lib.fqkv_version()
 
 
+def test_merge_diagnostics_before_any_call(lib):
+    """No split call has run in this process: no protocol, no fallback, no
+    XCD period; a device index out of range reads as unusable."""
+    lib.fqkv_merge_fallback_count.restype = ctypes.c_int64
+    assert lib.fqkv_last_merge_protocol() == 0
+    assert lib.fqkv_merge_fallback_count() == 0
+    assert lib.fqkv_xcd_period(0) == 0
+    assert lib.fqkv_xcd_period(-1) == -1 and lib.fqkv_xcd_period(64) == -1
+
+
 def _err(lib):
     return lib.fqkv_last_error().decode()
 

@@ -22,6 +22,7 @@ pytestmark = pytest.mark.gpu
 
 TOL = 2e-3
 DEV = "cuda"
+NONE, TWO_KERNEL, DEVICE, XCD_LOCAL = 0, 1, 2, 3  # FQKV_MERGE_*
 
 
 def draw(g, *shape):
@@ -121,15 +122,22 @@ def test_more_streams_than_merge_slots():
     streams = [torch.cuda.Stream() for _ in range(20)]
     for s in streams:
         s.wait_stream(torch.cuda.current_stream())
+    before = fq._ext._merge_fallback_count()
+    protocols = set()
     for rep in range(3):
         for c, s in zip(calls, streams):
             with torch.cuda.stream(s):
                 run(c)
+            protocols.add(fq._ext._last_merge_protocol())
     for s in streams:
         torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     for c, ref in zip(calls, alone):
         assert torch.equal(c[4], ref)
+    # the streams past the eager slots were counted, and their calls took the two-kernel merge
+    assert fq._ext._merge_fallback_count() > before
+    # streams with a slot read a full CU mask and take the XCD-local merge (8 head groups, 16 splits)
+    assert TWO_KERNEL in protocols and XCD_LOCAL in protocols and DEVICE not in protocols, protocols
 
 
 @pytest.mark.parametrize("S", [5, 17, 31, 32, 40])
@@ -198,9 +206,12 @@ def test_xcd_local_merge_alternating_inputs(Hkv, N, D, S):
     scratch, o = a[3], a[4]
     b = b[:3] + (scratch, o, S)
     first = {}
+    # 4 query heads per KV row make one head group per row: Hkv groups
+    expect = XCD_LOCAL if Hkv % 8 == 0 else DEVICE
     for i in range(12):
         c = (a, b)[i % 2]
         run(c)
+        assert fq._ext._last_merge_protocol() == expect, (i, fq._ext._last_merge_protocol())
         torch.cuda.synchronize()
         if i < 2:
             first[i] = (o.clone(), scratch[2].clone())
@@ -210,6 +221,7 @@ def test_xcd_local_merge_alternating_inputs(Hkv, N, D, S):
     try:
         for i in (0, 1):
             run((a, b)[i])
+            assert fq._ext._last_merge_protocol() == TWO_KERNEL
             torch.cuda.synchronize()
             assert torch.equal(scratch[2], first[i][1]), f"partials of input {i}"
     finally:
@@ -219,3 +231,89 @@ def test_xcd_local_merge_alternating_inputs(Hkv, N, D, S):
         ref = oracle.gqa_attention(q[None], K[None], V[None])[0]
         err = np.abs(first[i][0].cpu().double().numpy() - ref).max()
         assert err <= TOL, (i, err)
+
+
+def test_xcd_probe_found_the_round_robin_order():
+    """MI355X deals a launch's workgroups to its 8 XCDs in turn; the probe that
+    the first eager split call ran must have found exactly that period."""
+    g = torch.Generator().manual_seed(65)
+    run(make_call(g, N=4096, S=32))
+    torch.cuda.synchronize()
+    assert fq._ext._xcd_period(torch.cuda.current_device()) == 8
+
+
+def test_forked_streams_in_one_capture_take_separate_slots():
+    """Two split calls captured on forked streams of one graph (the side
+    stream joins the capture through an event wait, so both report the same
+    capture id) run side by side on replay; each must have its own arrival
+    counters. Every replay equals the eager results bit for bit."""
+    g = torch.Generator().manual_seed(66)
+    a = make_call(g, N=6000, S=32)
+    b = make_call(g, N=7000, S=32)
+    run(a)
+    ref_a = a[4].clone()
+    run(b)
+    ref_b = b[4].clone()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cur = torch.cuda.current_stream()
+        side.wait_stream(cur)
+        run(a)
+        with torch.cuda.stream(side):
+            run(b)
+        cur.wait_stream(side)
+    for _ in range(10):
+        a[4].zero_()
+        b[4].zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(a[4], ref_a)
+        assert torch.equal(b[4], ref_b)
+    # eager calls afterwards are unaffected
+    run(a)
+    torch.cuda.synchronize()
+    assert torch.equal(a[4], ref_a)
+
+
+def test_cu_masked_stream_keeps_the_device_scope_merge():
+    """A stream created with a CU mask that leaves half the CUs out may deal
+    workgroups to the XCDs in another order, so its split calls take the
+    device-scope merge; the output equals an unmasked stream's bit for bit."""
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    L = ctypes.CDLL(fq.lib_path())
+    VP, I64 = ctypes.c_void_p, ctypes.c_int64
+    L.fqkv_gqa_sk_fast.argtypes = [VP] * 7 + [I64] * 7 + [VP]
+    L.fqkv_last_error.restype = ctypes.c_char_p
+    g = torch.Generator().manual_seed(67)
+    Hq, Hkv, N, D, S = 32, 8, 8192, 128, 32
+    q, K, V, (mp, lp, op), o, _ = make_call(g, Hq=Hq, Hkv=Hkv, N=N, D=D, S=S)
+    args = [x.data_ptr() for x in (q, K, V, mp, lp, op, o)] + [Hq, Hkv, N, D, S, 8, 8]
+    torch.cuda.synchronize()
+    assert L.fqkv_gqa_sk_fast(*args, torch.cuda.current_stream().cuda_stream) == 0, L.fqkv_last_error()
+    assert L.fqkv_last_merge_protocol() == XCD_LOCAL
+    torch.cuda.synchronize()
+    ref = o.clone()
+    words = (fq._ext._cu_count() + 31) // 32
+    mask = (ctypes.c_uint32 * words)(*([0x55555555] * words))
+    st = ctypes.c_void_p()
+    rc = hip.hipExtStreamCreateWithCUMask(ctypes.byref(st), ctypes.c_uint32(words), mask)
+    if rc != 0:
+        # a CU-masked stream needs a hardware queue of its own; a runtime limited
+        # to a few queues per process (GPU_MAX_HW_QUEUES) refuses one. The refusal
+        # stays pending as HIP's last error, which the next HIP call would report.
+        hip.hipGetLastError()
+        assert hip.hipGetLastError() == 0
+        pytest.skip("hipExtStreamCreateWithCUMask failed with HIP error %d on this system" % rc)
+    try:
+        for _ in range(3):
+            o.zero_()
+            torch.cuda.synchronize()
+            assert L.fqkv_gqa_sk_fast(*args, st) == 0, L.fqkv_last_error()
+            assert L.fqkv_last_merge_protocol() == DEVICE
+            assert hip.hipStreamSynchronize(st) == 0
+            assert torch.equal(o, ref)
+    finally:
+        hip.hipStreamDestroy(st)
