@@ -19,8 +19,13 @@ on (PyTorch's current stream). With --merge two-kernel the partial kernel is
 timed per launch with HIP events recorded just around it. ``cpu_baseline``
 times the reference's CPU path (repeat_interleave + scaled_dot_product_attention
 on CPU tensors, every host thread) on a bounded sample of the same workload.
-Further keys carry the reference's other benchmark shapes (MHA fp16 / int8 /
-int4 at B=2048, N=4096, D=128; split-K at B=8, N=32768; the launch floor).
+Further keys carry the reference's other benchmark shapes: MHA fp16 / int8 /
+int4 at B=2048, N=4096, D=128; split-K at B=8, N=32768; the launch floor; the
+reference's primary split-K table (D in {64, 128} x N in {512 .. 32768}, each
+point swept over S/W/CW under the correctness gate); the remaining BASELINE
+rows at D=128 (MHA B=32 N=512; fp16 / int8 / int4 MHA at B=8 and 256; GQA at
+N=512, D=64 against repeat_kv + MHA; int8 / int4 split-K at the headline
+shape); and the reference's D=64 tables with its A100 numbers alongside.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--S S --W W --CW CW]
        python bench.py --sweep      (tuning table on stderr, then the JSON line)
@@ -116,6 +121,13 @@ def gate(torch, fq, q, K, V, S, W, CW):
     return float((o.float() - ref).abs().max())
 
 
+# Warm-up calls queued after the synchronisation that precedes a timed region: the GPU is running
+# real calls when the start event is queued, so the timed calls follow back to back instead of
+# starting on an idle GPU behind the host's launch latency of the first one (about 10 us through
+# Python, half a microsecond per call when only 20 calls are timed). They lie outside the region.
+LEAD_CALLS = 4
+
+
 def time_calls(torch, fq, q, Ks, Vs, S, W, CW, steps, warmup):
     mp = torch.empty(HQ, S, device="cuda")
     lp = torch.empty(HQ, S, device="cuda")
@@ -125,6 +137,8 @@ def time_calls(torch, fq, q, Ks, Vs, S, W, CW, steps, warmup):
     for i in range(warmup):
         fq.gqa_sk_fast(q, Ks[i % n], Vs[i % n], mp, lp, op, o, S, W, CW)
     torch.cuda.synchronize()
+    for i in range(LEAD_CALLS):
+        fq.gqa_sk_fast(q, Ks[i % n], Vs[i % n], mp, lp, op, o, S, W, CW)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for i in range(steps):
@@ -368,6 +382,8 @@ def _loop_ms(torch, fn, nsets, steps, warmup):
     for i in range(warmup):
         fn(i % nsets)
     torch.cuda.synchronize()
+    for i in range(LEAD_CALLS):
+        fn(i % nsets)
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for i in range(steps):
@@ -579,13 +595,14 @@ def suite_mha_small(torch, fq, steps, warmup, rows):
     log("mha_fp16  B=%d N=%d D=%d  %8.2f us  %7.1f GB/s  err %.2e" % (B, N, Dm, ms * 1e3, nbytes / ms / 1e6, err))
 
 
-def suite_splitk_quant(torch, fq, steps, warmup, rows):
+def suite_splitk_quant(torch, fq, steps, warmup, rows, cases=((1, 16384), (8, 32768)), formats=("int8", "int4", "fp8")):
     """gqa_sk_fast_int8 / _int4 (Hq 32, Hkv 8, D 128) at N 16384 (batch 1) and B 8, N 32768:
-    long-context decode over a quantized cache, best of a small S/W sweep."""
+    long-context decode over a quantized cache, best of a small S/W sweep; cases: (B, N) pairs,
+    formats: a subset of int8, int4, fp8."""
     Hq, Hkv, Dd = 32, 8, 128
     G = Hq // Hkv
-    for B, N in ((1, 16384), (8, 32768)):
-        for fmt in ("int8", "int4", "fp8"):
+    for B, N in cases:
+        for fmt in formats:
             g = torch.Generator(device="cuda").manual_seed(5)
             quantize = {"int8": fq.quantize_int8_per_token, "int4": fq.quantize_int4_per_token,
                         "fp8": fq.quantize_fp8_per_token}[fmt]
@@ -934,6 +951,123 @@ SUITES = ("mha_small", "mha_quant", "gqa", "splitk", "splitk_quant", "paged", "q
 REF_E2E_TOK_S = (51.887, 54.680)
 
 
+# The reference's primary table on its A100 (benchmarks/flashinfer_looptimed.json:6-149): gqa_sk_fast
+# at Hq 32 / Hkv 8, batch 1, loop-timed µs per call and the best S/W/CW of its sweep, per (D, N).
+REF_SPLITK_A100 = {
+    (64, 512): (10.48, "S16W8C4"), (64, 1024): (12.57, "S16W8C4"), (64, 2048): (16.93, "S16W8C4"),
+    (64, 4096): (25.05, "S32W8C8"), (64, 8192): (39.23, "S32W8C8"), (64, 16384): (94.30, "S128W8C8"),
+    (128, 512): (11.86, "S16W8C4"), (128, 1024): (14.71, "S16W8C4"), (128, 2048): (20.11, "S16W8C4"),
+    (128, 4096): (30.63, "S16W8C4"), (128, 8192): (74.25, "S64W8C8"), (128, 16384): (129.34, "S128W8C8"),
+}
+MERGE_NAMES = {0: "none (one split)", 1: "two-kernel", 2: "fused, device scope", 3: "fused, one XCD's L2"}
+
+
+def splitk_primary_table(torch, fq, sweep_steps=200, sweep_warmup=20, steps=2000, warmup=200):
+    """The reference's primary benchmark at its own shapes, plus N = 32768 (flashinfer_looptimed.py:59-95):
+    gqa_sk_fast, Hq 32 / Hkv 8, batch 1, D in {64, 128}, N in {512 .. 32768}. Every S in
+    {8, 16, 32, 64, 128} (S <= N / 16), W in {4, 8} and CW in {4, 8} that passes the correctness gate
+    (max-abs <= 2e-3 against fp32 PyTorch on the GPU; the reference gates at 2e-2) is loop-timed over
+    `sweep_steps` calls; the fastest is timed again over `steps` calls after `warmup`, as the reference
+    does (2000 after 200). Each point cycles through >= 512 MiB of distinct KV sets (at most 512), so
+    the Infinity Cache cannot serve a call from the previous one. CW sizes the combine kernel of the
+    two-kernel merge; the default fused merge launches none, so CW does not change those calls."""
+    G = HQ // HKV
+    table = {}
+    for Dd in (64, 128):
+        for Nn in (512, 1024, 2048, 4096, 8192, 16384, 32768):
+            per = 4 * HKV * Nn * Dd
+            ns = max(1, min(512, -(-(512 << 20) // per)))
+            g = torch.Generator(device="cuda").manual_seed(7)
+            q = torch.randn(HQ, Dd, device="cuda", generator=g).half()
+            sets = [(torch.randn(HKV, Nn, Dd, device="cuda", generator=g).half(),
+                     torch.randn(HKV, Nn, Dd, device="cuda", generator=g).half()) for _ in range(ns)]
+            ref = _ref_mha(torch, q, sets[0][0].float().repeat_interleave(G, 0),
+                           sets[0][1].float().repeat_interleave(G, 0))
+            nbytes = alg_bytes(n=Nn, d=Dd)
+            best = None
+            for S in (8, 16, 32, 64, 128):
+                if S > Nn // 16:
+                    continue
+                mp = torch.empty(HQ, S, device="cuda")
+                lp = torch.empty(HQ, S, device="cuda")
+                op = torch.empty(HQ, S, Dd, device="cuda")
+                o = torch.empty(HQ, Dd, device="cuda", dtype=torch.float16)
+                for Wk in (4, 8):
+                    for CW in (4, 8):
+                        fn = lambda i: fq.gqa_sk_fast(q, sets[i][0], sets[i][1], mp, lp, op, o, S, Wk, CW)
+                        fn(0)
+                        proto = fq._ext._last_merge_protocol()
+                        err = float((o.float() - ref).abs().max())
+                        if err > 2e-3:
+                            log("split-K D=%d N=%d S%d W%d CW%d failed the gate: %.2e" % (Dd, Nn, S, Wk, CW, err))
+                            continue
+                        ms = _loop_ms(torch, fn, ns, sweep_steps, sweep_warmup)
+                        if best is None or ms < best[0]:
+                            best = (ms, S, Wk, CW, err, proto, (mp, lp, op, o))
+            _, S, Wk, CW, err, proto, (mp, lp, op, o) = best
+            ms = _loop_ms(torch, lambda i: fq.gqa_sk_fast(q, sets[i][0], sets[i][1], mp, lp, op, o, S, Wk, CW),
+                          ns, steps, warmup)
+            row = {"us_per_call": round(ms * 1e3, 3), "GBps": round(nbytes / ms / 1e6, 1), "frac": _frac(nbytes, ms),
+                   "alg_bytes": nbytes, "kv_GBps": round(2 * Nn * HKV * Dd * 2 / ms / 1e6, 1),
+                   "best": "S%dW%dC%d" % (S, Wk, CW), "merge": MERGE_NAMES[proto], "kv_sets": ns,
+                   "kv_bytes_cycled": ns * per, "gate_max_abs_err": err}
+            if (Dd, Nn) in REF_SPLITK_A100:
+                ref_us, ref_cfg = REF_SPLITK_A100[(Dd, Nn)]
+                row.update({"ref_a100_us": ref_us, "ref_a100_best": ref_cfg, "speedup_vs_ref_a100": round(ref_us / (ms * 1e3), 2)})
+            table["D%d_N%d" % (Dd, Nn)] = row
+            log("primary table D=%-3d N=%-6d %s  %8.2f us  %7.1f GB/s (%.1f %% of 8 TB/s)  err %.2e"
+                % (Dd, Nn, row["best"], ms * 1e3, nbytes / ms / 1e6, 100 * row["frac"], err))
+            del sets, ref
+            torch.cuda.empty_cache()
+    return table
+
+
+def baseline_rows(torch, fq):
+    """BASELINE.md section 2 rows beside the headline, the B = 2048 MHA rows and the primary table:
+    * mha_fp16_b32_n512_d128: fp16 MHA, 32 heads, N 512, D 128 (the reference's CPU-runnable case);
+    * mha_n4096_d128: fp16 / int8 / int4 MHA at B 8 and 256, N 4096, D 128 (B 2048 is
+      mha_b2048_n4096_d128);
+    * gqa_n512_d64: decode_attn_gqa vs repeat_kv + the MHA kernel at Hq 32 / Hkv 8, N 512, D 64,
+      B in {1, 4, 16};
+    * splitk_quant_n16384_d128: gqa_sk_fast_int8 / _int4 at the headline shape (Hq 32 / Hkv 8,
+      N 16384, D 128, batch 1), best of S in {16, 32, 64} x W in {4, 8}.
+    Loop-timed (400 calls after 40 warm-ups) over >= 1 GiB of distinct inputs per cycle, each row
+    gated against fp32 PyTorch on the GPU (max-abs <= 2e-3)."""
+    out = {}
+    rows = []
+    suite_mha_small(torch, fq, 400, 40, rows)
+    r = rows[0]
+    out["mha_fp16_b32_n512_d128"] = {"us_per_call": r["us_per_call"], "GBps": r["GBps"], "frac": r["frac_of_8TBps"],
+                                     "alg_bytes": r["alg_bytes"], "gate_max_abs_err": r["max_abs_err_vs_fp32"]}
+    rows = []
+    suite_mha_quant(torch, fq, 400, 40, rows, shapes=[(128, 8), (128, 256)], formats=("fp16", "int8", "int4"))
+    mq = {}
+    for r in rows:
+        fmt, B = r["bench"].split("_")[1], r["config"]["B"]
+        mq.setdefault("B%d" % B, {})[fmt] = {"us_per_call": r["us_per_call"], "GBps": r["GBps"],
+                                             "frac": r["frac_of_8TBps"], "alg_bytes": r["alg_bytes"],
+                                             "gate_max_abs_err": r["max_abs_err_vs_fp32"]}
+    out["mha_n4096_d128"] = mq
+    rows = []
+    suite_gqa(torch, fq, 400, 40, rows, shapes=[(512, b) for b in (1, 4, 16)])
+    out["gqa_n512_d64"] = {"B%d" % r["config"]["B"]: {"gqa_us": r["us_per_call"], "GBps": r["GBps"],
+                                                      "frac": r["frac_of_8TBps"],
+                                                      "repeat_kv_mha_us": r["expand_mha_us"],
+                                                      "speedup_vs_repeat_kv": r["speedup_vs_expand"],
+                                                      "gate_max_abs_err": r["max_abs_err_vs_fp32"]} for r in rows}
+    rows = []
+    suite_splitk_quant(torch, fq, 400, 40, rows, cases=((1, 16384),), formats=("int8", "int4"))
+    out["splitk_quant_n16384_d128"] = {r["bench"].rsplit("_", 1)[1]: {
+        "us_per_call": r["us_per_call"], "GBps": r["GBps"], "frac": r["frac_of_8TBps"], "alg_bytes": r["alg_bytes"],
+        "S": r["config"]["S"], "W": r["config"]["W"], "gate_max_abs_err": r["max_abs_err_vs_fp32"]} for r in rows}
+    for name, r in out.items():
+        for v in ([r] if "gate_max_abs_err" in r else r.values()):
+            for x in ([v] if "gate_max_abs_err" in v else v.values()):
+                if x["gate_max_abs_err"] > 2e-3:
+                    raise RuntimeError("baseline-row gate failed: %s max-abs %.3e" % (name, x["gate_max_abs_err"]))
+    return out
+
+
 def reference_tables(torch, fq):
     """The reference's other published tables at their own shapes, for the default line:
     * standalone_quant_d64 (benchmarks/standalone_quant.json): fp16 / int8 / int4 MHA at
@@ -1031,7 +1165,8 @@ def main():
                          "(fp16, D 128, 1 or 4 heads per work item)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
-                    help="skip the secondary keys (MHA B=2048, split-K B=8 N=32K, launch floor)")
+                    help="skip the secondary keys (MHA B=2048, split-K B=8 N=32K, launch floor, primary "
+                         "split-K table, BASELINE rows, the reference's D=64 tables)")
     ap.add_argument("--suite", metavar="FILE", default="",
                     help="also measure the secondary configurations, JSON lines into FILE")
     ap.add_argument("--suite-only", metavar="NAMES", default=",".join(SUITES),
@@ -1090,14 +1225,17 @@ def main():
     if err > 2e-3:
         log("correctness gate failed: max-abs %.3e > 2e-3" % err)
         sys.exit(1)
+    merge_protocol = fq._ext._last_merge_protocol()
 
     ms = time_calls(torch, fq, q, Ks, Vs, S, W, CW, args.steps, args.warmup)
+    ms_long = time_calls(torch, fq, q, Ks, Vs, S, W, CW, 2000, 200) if args.steps < 2000 else ms
     ev = HipEvents()
     p_avg_ms, p_med_ms = time_partial(torch, fq, q, Ks, Vs, S, W, CW, min(args.steps, 1000), ev)
     value = alg_bytes() / ms / 1e6  # GB/s
     if args.merge == "fused":
         # one kernel per call: its average duration is the loop time per call
-        k_ms, method = ms, "HIP events around the timed loop of %d calls, one kernel per call" % args.steps
+        k_ms, method = ms, ("HIP events around the timed loop of %d calls, one kernel per call; %d more warm-up "
+                            "calls queued after the synchronisation, ahead of the start event" % (args.steps, LEAD_CALLS))
     else:
         k_ms, method = p_avg_ms, "HIP events recorded just before and after each partial launch"
     achieved = alg_bytes() / k_ms / 1e6
@@ -1112,6 +1250,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
         "us_per_call": round(ms * 1e3, 3),
+        "us_per_call_2000_calls": round(ms_long * 1e3, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": round(value / REF_A100_GBS, 3) if N == 16384 else None,
@@ -1121,7 +1260,8 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "gqa_sk_fast fp16 decode, Hq=32, Hkv=8, N=%d, D=128, batch 1" % N,
-            "S": S, "W": W, "CW": CW, "merge": args.merge, "pv": args.pv,
+            "S": S, "W": W, "CW": CW, "merge": MERGE_NAMES[merge_protocol], "pv": args.pv,
+            "xcd_period": fq._ext._xcd_period(torch.cuda.current_device()),
             "kv_sets": args.kv_sets,
             "kv_bytes_cycled": args.kv_sets * 4 * HKV * N * D,
             "alg_bytes_per_call": alg_bytes(),
@@ -1137,6 +1277,8 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBS, 4),
             "traffic": traffic,
+            "traffic_source": ("profiles/decode_partial_gqa_n16k_d128_pmc.md (rocprofv3 --pmc FETCH_SIZE + "
+                               "WRITE_SIZE of this kernel, committed; not measured in this run)") if traffic else None,
             "avg_us": round(k_ms * 1e3, 3),
             "method": method,
             "per_launch_event_avg_us": round(p_avg_ms * 1e3, 3),
@@ -1154,6 +1296,8 @@ def main():
         % (ceil["blocks"], ceil["us_per_call"], ceil["GBps"], 100 * ceil["headline_frac_of_ceiling"]))
     if not args.no_secondary:
         line.update(secondary_results(torch, fq))
+        line["splitk_primary_table"] = splitk_primary_table(torch, fq)
+        line["baseline_d128_rows"] = baseline_rows(torch, fq)
         line["reference_tables"] = reference_tables(torch, fq)
     if args.suite:
         run_suite(torch, fq, args.suite, only=only)
