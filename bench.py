@@ -31,6 +31,10 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--S S --W W --CW CW]
        python bench.py --sweep      (tuning table on stderr, then the JSON line)
        python bench.py --suite FILE (secondary configurations as JSON lines in
                                      FILE and a table on stderr, then the JSON line)
+       python bench.py --timeline [--n-tokens N --S S]
+                                    (where a call's time goes: host issue, loop and
+                                     graph-replay cost per call, and the kernel's
+                                     per-stage clock stamps; one JSON line)
 """
 
 import argparse
@@ -962,6 +966,163 @@ REF_SPLITK_A100 = {
 MERGE_NAMES = {0: "none (one split)", 1: "two-kernel", 2: "fused, device scope", 3: "fused, one XCD's L2"}
 
 
+# ---------------------------------------------------------------------------
+# Where a call's time goes (--timeline): the decode kernel's own clock stamps
+# beside the host's issue cost and the GPU's back-to-back cost per call.
+
+# stage index of the stamps -> what has happened when a wave writes it
+TIMELINE_STAGES = (
+    (0, "wave started"),
+    (1, "every K/V load of the first pass issued"),
+    (3, "last pass's P.V products issued"),
+    (4, "wave totals written to LDS"),
+    (5, "wave-merge barrier passed"),
+    (6, "output or partials issued"),
+    (7, "arrival known"),
+    (8, "merge: maximum over the splits known"),
+    (9, "merge done"),
+    (10, "wave ended"),
+)
+TL_BLOCKS, TL_WAVES, TL_SLOTS = 4096, 8, 16  # g_timeline's shape in the stamped build
+
+
+def _stage_stats(x):
+    x = sorted(x)
+    n = len(x)
+    return {"n": n, "min": round(x[0], 2), "p10": round(x[n // 10], 2), "median": round(x[n // 2], 2),
+            "p90": round(x[n * 9 // 10], 2), "max": round(x[-1], 2)}
+
+
+def timeline_stamps(torch, q, Ks, Vs, S, W, CW, calls=30, reps=3):
+    """Stage stamps of the last of `calls` back-to-back gqa_sk_fast calls, from
+    libfqkv_decode_timeline.so (the same kernels built with -DFQKV_TIMELINE:
+    lane 0 of every wave reads the 100 MHz real-time counter at each stage).
+    Times are microseconds from the earliest wave start of that call; the
+    median over `reps` repetitions of each statistic is reported."""
+    import numpy as np
+    from fqkv_decode._paths import PKG_DIR, TIMELINE_LIB_NAME
+
+    path = os.path.join(PKG_DIR, TIMELINE_LIB_NAME)
+    if not os.path.exists(path):
+        raise SystemExit("%s is missing: build first (python -c 'import __graft_entry__ as g; g.build()')" % path)
+    lib = ctypes.CDLL(path)
+    call = lib.fqkv_gqa_sk_fast
+    call.restype = ctypes.c_int
+    call.argtypes = [ctypes.c_void_p] * 7 + [ctypes.c_int64] * 7 + [ctypes.c_void_p]
+    read = lib.fqkv_timeline_read
+    read.restype = ctypes.c_int
+    read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    hq, n_tok, d = q.shape[0], Ks[0].shape[1], q.shape[1]
+    hkv = Ks[0].shape[0]
+    mp = torch.empty(hq, S, device="cuda")
+    lp = torch.empty(hq, S, device="cuda")
+    op = torch.empty(hq, S, d, device="cuda")
+    o = torch.empty(hq, d, device="cuda", dtype=torch.float16)
+    stream = torch.cuda.current_stream().cuda_stream
+    buf = np.zeros((TL_BLOCKS, TL_WAVES, TL_SLOTS), dtype=np.uint64)
+    per_rep = []
+    for rep in range(reps):
+        torch.cuda.synchronize()
+        if read(None, ctypes.c_size_t(-1).value) != 0:
+            raise RuntimeError("fqkv_timeline_read (clear) failed")
+        for i in range(calls):
+            j = (rep * calls + i) % len(Ks)
+            rc = call(q.data_ptr(), Ks[j].data_ptr(), Vs[j].data_ptr(), mp.data_ptr(), lp.data_ptr(),
+                      op.data_ptr(), o.data_ptr(), hq, hkv, n_tok, d, S, W, CW, stream)
+            if rc != 0:
+                raise RuntimeError("timeline build: fqkv_gqa_sk_fast returned %d" % rc)
+        torch.cuda.synchronize()
+        if read(buf.ctypes.data, buf.nbytes) != 0:
+            raise RuntimeError("fqkv_timeline_read failed")
+        start = buf[:, :, 0]
+        t0 = start[start > 0].min()
+        # stamps older than the last call's first wave were left by earlier calls
+        # (a workgroup that merged then but not in the last call)
+        stages = {}
+        for idx, name in TIMELINE_STAGES:
+            v = buf[:, :, idx]
+            v = v[v >= t0]
+            if v.size:
+                stages[idx] = _stage_stats(((v - t0).astype(np.float64) / 100.0).tolist())
+        merged = np.nonzero((buf[:, :, 9] >= t0).any(axis=1))[0]
+        end = buf[:, :, 10]
+        span = float((end[end >= t0].max() - t0) / 100.0)
+        per_rep.append((stages, span, len(merged), int((start > 0).any(axis=1).sum())))
+    out = {"calls": calls, "reps": reps, "workgroups": per_rep[0][3], "merging_workgroups": per_rep[0][2]}
+    out["span_us"] = round(sorted(r[1] for r in per_rep)[reps // 2], 2)
+    stages = {}
+    for idx, name in TIMELINE_STAGES:
+        rows = [r[0][idx] for r in per_rep if idx in r[0]]
+        if not rows:
+            continue
+        st = {k: (sorted(r[k] for r in rows)[len(rows) // 2]) for k in rows[0]}
+        st["stage"] = idx
+        stages[name] = st
+    out["stages_us"] = stages
+    return out
+
+
+def launch_costs(torch, fq, q, Ks, Vs, S, W, CW, steps=2000, warmup=200, graph_calls=100, replays=20):
+    """Per-call cost of the same gqa_sk_fast call three ways:
+    * loop_us: the bench's Python loop between HIP events (the headline method);
+    * host_issue_us: host wall time to issue one call of that loop (nothing
+      waits for the GPU inside it), i.e. the rate at which the host can feed
+      the GPU through the PyTorch binding;
+    * graph_us: `graph_calls` calls captured in one HIP graph and replayed
+      `replays` times between events, so no host work sits between launches:
+      the GPU's own back-to-back cost per call (dispatch + kernel)."""
+    hq, d = q.shape
+    mp = torch.empty(hq, S, device="cuda")
+    lp = torch.empty(hq, S, device="cuda")
+    op = torch.empty(hq, S, d, device="cuda")
+    o = torch.empty(hq, d, device="cuda", dtype=torch.float16)
+    n = len(Ks)
+    fn = lambda i: fq.gqa_sk_fast(q, Ks[i % n], Vs[i % n], mp, lp, op, o, S, W, CW)
+    loop_ms = _loop_ms(torch, fn, n, steps, warmup)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for i in range(steps):
+        fn(i)
+    issue_s = time.perf_counter() - t
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(3):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(graph_calls):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    graph_ms = a.elapsed_time(b) / (replays * graph_calls)
+    del graph
+    fq._ext._release_capture_slots()
+    return {"loop_us": round(loop_ms * 1e3, 3), "host_issue_us": round(issue_s / steps * 1e6, 3),
+            "graph_us": round(graph_ms * 1e3, 3), "graph_calls": graph_calls, "replays": replays}
+
+
+def timeline_report(torch, fq, q, Ks, Vs, S, W, CW):
+    res = {"launch_costs": launch_costs(torch, fq, q, Ks, Vs, S, W, CW),
+           "timeline": timeline_stamps(torch, q, Ks, Vs, S, W, CW)}
+    lc, tl = res["launch_costs"], res["timeline"]
+    log("per call: Python loop %.3f us, host issue %.3f us, graph replay %.3f us; in-kernel span %.2f us "
+        "(%d workgroups, %d merging)" % (lc["loop_us"], lc["host_issue_us"], lc["graph_us"], tl["span_us"],
+                                         tl["workgroups"], tl["merging_workgroups"]))
+    for name, st in tl["stages_us"].items():
+        log("  stage %2d %-42s n %5d  min %6.2f  p10 %6.2f  median %6.2f  p90 %6.2f  max %6.2f"
+            % (st["stage"], name, st["n"], st["min"], st["p10"], st["median"], st["p90"], st["max"]))
+    return res
+
+
 def splitk_primary_table(torch, fq, sweep_steps=200, sweep_warmup=20, steps=2000, warmup=200):
     """The reference's primary benchmark at its own shapes, plus N = 32768 (flashinfer_looptimed.py:59-95):
     gqa_sk_fast, Hq 32 / Hkv 8, batch 1, D in {64, 128}, N in {512 .. 32768}. Every S in
@@ -1171,6 +1332,9 @@ def main():
                     help="also measure the secondary configurations, JSON lines into FILE")
     ap.add_argument("--suite-only", metavar="NAMES", default=",".join(SUITES),
                     help="comma-separated subset of the suite: " + ", ".join(SUITES))
+    ap.add_argument("--timeline", action="store_true",
+                    help="instead of the benchmark line: per-call host issue / Python loop / graph replay cost and "
+                         "the decode kernel's per-stage clock stamps (libfqkv_decode_timeline.so) for the workload")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB (counter calibration under rocprofv3 --pmc)")
     args = ap.parse_args()
@@ -1226,6 +1390,13 @@ def main():
         log("correctness gate failed: max-abs %.3e > 2e-3" % err)
         sys.exit(1)
     merge_protocol = fq._ext._last_merge_protocol()
+    if args.timeline:
+        res = timeline_report(torch, fq, q, Ks, Vs, S, W, CW)
+        res["config"] = {"workload": "gqa_sk_fast fp16 decode, Hq=32, Hkv=8, N=%d, D=128, batch 1" % N,
+                         "S": S, "W": W, "CW": CW, "merge": MERGE_NAMES[merge_protocol], "kv_sets": args.kv_sets,
+                         "gate_max_abs_err": err}
+        print(json.dumps(res), flush=True)
+        return
 
     ms = time_calls(torch, fq, q, Ks, Vs, S, W, CW, args.steps, args.warmup)
     ms_long = time_calls(torch, fq, q, Ks, Vs, S, W, CW, 2000, 200) if args.steps < 2000 else ms

@@ -5,6 +5,8 @@ import sysconfig
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = "libfqkv_decode.so"
+# the same library built with per-stage clock stamps in the decode kernel (diagnostics only)
+TIMELINE_LIB_NAME = "libfqkv_decode_timeline.so"
 EXT_NAME = "_fqkv_torch"
 
 
