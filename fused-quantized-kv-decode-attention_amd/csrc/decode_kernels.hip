@@ -509,76 +509,125 @@ template <int D>
 constexpr int opitch() { return D + 4; }
 
 // Merge the NWC waves' (m, l, acc) of a workgroup through LDS and emit the
-// normalised fp16 output (one split) or the split's fp32 partials. Thread
-// (head h, element d) forms the waves' weights e^(m_w - M) itself from the
-// head's LDS row; an empty wave (m = -inf) weighs 0 and an empty split keeps
-// M = -inf with l = acc = 0. All LDS reads are in flight together. A wave
-// covers one head (D threads per head, D >= 64), so the head's global row
-// address is wave-uniform.
+// normalised fp16 output (one split) or the split's fp32 partials. Thread t
+// takes four consecutive elements 4t .. 4t+3 of the workgroup's hcnt x D
+// outputs (head h = 4t / D): one pass whenever HG x D <= 256 x waves (every
+// shape here with 4 or 8 waves; 4 heads of 128 with 2 waves, the one-token
+// split, took four passes at one element per thread, 1.6 us of a 5 us
+// call). Each thread forms its head's wave weights
+// e^(m_w - M) itself from the head's LDS rows (read whole; every lane of a head
+// reads the same address), adds the NWC waves' float4 of acc, and stores 16
+// bytes of partials or four fp16 outputs. An empty wave (m = -inf) weighs 0
+// and an empty split keeps M = -inf with l = acc = 0. The l sum is the
+// pairwise tree (w0 l0 + w1 l1) + (w2 l2 + w3 l3) + ..., the acc sum goes
+// wave by wave.
+template <int N>
+__device__ __forceinline__ void lds_row(const float* src, float (&v)[N]) {
+  if constexpr (N == 2) {
+    const float2 a = *reinterpret_cast<const float2*>(src);
+    v[0] = a.x;
+    v[1] = a.y;
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      const fl4_t a = *reinterpret_cast<const fl4_t*>(src + i);
+      v[i] = a.x;
+      v[i + 1] = a.y;
+      v[i + 2] = a.z;
+      v[i + 3] = a.w;
+    }
+  }
+}
+template <int N>
+__device__ __forceinline__ float tree_sum(const float (&v)[N]) {
+  if constexpr (N == 2) {
+    return v[0] + v[1];
+  } else if constexpr (N == 4) {
+    return (v[0] + v[1]) + (v[2] + v[3]);
+  } else {
+    return ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  }
+}
+
 template <int D, int HG, int NWC>
 __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const float (*s_o)[HG][opitch<D>()],
                                                  const float (*s_m)[NW_MAX], const float (*s_l)[NW_MAX],
                                                  size_t qrow0, int hcnt, int s) {
-  const int lane = threadIdx.x & 63;
-  for (int idx = threadIdx.x; idx < hcnt * D; idx += blockDim.x) {
-    const int h = __builtin_amdgcn_readfirstlane(idx / D);
-    const int d = idx % D;
-    // the head's wave weights once per wave: lane j < NWC holds wave j's (m, l)
-    const float mj = lane < NWC ? s_m[h][lane & (NWC - 1)] : -INFINITY;
-    const float lj = lane < NWC ? s_l[h][lane & (NWC - 1)] : 0.0f;
-    int k = fkey(mj);
-    k = max(k, dpp_i<0xB1>(k));
-    k = max(k, dpp_i<0x4E>(k));
-    if constexpr (NWC > 4) {  // fold the row's four quads (rotations by 4 and 8 lanes)
-      k = max(k, dpp_i<0x124>(k));
-      k = max(k, dpp_i<0x128>(k));
-    }
-    const float M = unkey(__builtin_amdgcn_readlane(k, 0));
+  static_assert(NWC == 2 || NWC == 4 || NWC == 8, "waves per workgroup");
+  for (int idx = 4 * (int)threadIdx.x; idx < hcnt * D; idx += 4 * (int)blockDim.x) {
+    const int h = idx / D;
+    const int d = idx - h * D;
+    float mw[NWC], lw[NWC];
+    lds_row<NWC>(s_m[h], mw);
+    lds_row<NWC>(s_l[h], lw);
+    float M = mw[0];
+#pragma unroll
+    for (int j = 1; j < NWC; ++j) M = fmaxf(M, mw[j]);
     const float Mu = (M == -INFINITY) ? 0.0f : M;
-    const float wj = lane < NWC ? fast_exp2((mj - Mu) * p.c) : 0.0f;
-    float lw = wj * lj;
-    lw += dpp_f<0xB1>(lw);
-    lw += dpp_f<0x4E>(lw);
-    if constexpr (NWC > 4) {
-      lw += dpp_f<0x124>(lw);
-      lw += dpp_f<0x128>(lw);
+    float wj[NWC], wl[NWC];
+#pragma unroll
+    for (int j = 0; j < NWC; ++j) {
+      wj[j] = fast_exp2((mw[j] - Mu) * p.c);
+      wl[j] = wj[j] * lw[j];
     }
-    const float L = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, lw), 0));
-    float O = 0.0f;
+    const float L = tree_sum<NWC>(wl);
+    fl4_t O = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ww = 0; ww < NWC; ++ww) {
-      const float sc = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wj), ww));
-      O = fmaf(sc, s_o[ww][h][d], O);
+      const fl4_t a = *reinterpret_cast<const fl4_t*>(&s_o[ww][h][d]);
+      O.x = fmaf(wj[ww], a.x, O.x);
+      O.y = fmaf(wj[ww], a.y, O.y);
+      O.z = fmaf(wj[ww], a.z, O.z);
+      O.w = fmaf(wj[ww], a.w, O.w);
     }
     const size_t qh = qrow0 + h;
+    // normalised fp16 output (an empty sequence gives zeros)
+    auto put_out = [&]() {
+      _Float16* dst = p.o + qh * D + d;
+      const float Ox = O.x, Oy = O.y, Oz = O.z, Ow = O.w;
+      dst[0] = L > 0.0f ? (_Float16)(Ox / L) : (_Float16)0.0f;
+      dst[1] = L > 0.0f ? (_Float16)(Oy / L) : (_Float16)0.0f;
+      dst[2] = L > 0.0f ? (_Float16)(Oz / L) : (_Float16)0.0f;
+      dst[3] = L > 0.0f ? (_Float16)(Ow / L) : (_Float16)0.0f;
+    };
     if (p.direct) {
-      p.o[qh * D + d] = L > 0.0f ? (_Float16)(O / L) : (_Float16)0.0f;  // an empty sequence gives zeros
+      put_out();
     } else {
       const size_t b = qh * p.S + s;
-      float* orow = p.o_part + b * D;
+      float* orow = p.o_part + b * D + d;
       const float mo = (M == -INFINITY) ? -INFINITY : M * p.scale;
-      if (p.slot >= 0 && p.xcd_local) {  // read by a workgroup on this XCD: its L2 is the meeting point
-        if (d == 0) {
-          __hip_atomic_store(p.m_part + b, mo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-          __hip_atomic_store(p.l_part + b, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (p.slot >= 0) {
+        // 16-byte stores of the lane's four partials through a descriptor
+        // from the wave's first head row (a wave spans at most 64 / (D / 4)
+        // heads; rows of consecutive heads lie S x D floats apart)
+        const int h0 = __builtin_amdgcn_readfirstlane(h);
+        const rsrc_t rP = make_rsrc(p.o_part + ((qrow0 + h0) * p.S + s) * D,
+                                    ((uint32_t)(64 * 4 / D - 1) * (uint32_t)p.S * D + D) * 4u);
+        const int off = ((h - h0) * p.S * D + d) * 4;
+        const u4_t bits = __builtin_bit_cast(u4_t, O);
+        if (p.xcd_local) {  // read by a workgroup on this XCD: its L2 is the meeting point
+          if (d == 0) {
+            __hip_atomic_store(p.m_part + b, mo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            __hip_atomic_store(p.l_part + b, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(bits, rP, off, 0, CPOL_SC0);
+        } else {  // device-scope stores: read by another workgroup of this launch
+          if (d == 0) {
+            __hip_atomic_store(p.m_part + b, mo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(p.l_part + b, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          __builtin_amdgcn_raw_buffer_store_b128(bits, rP, off, 0, CPOL_SC1);
         }
-        __hip_atomic_store(orow + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      } else if (p.slot >= 0) {  // device-scope stores: read by another workgroup of this launch
-        if (d == 0) {
-          __hip_atomic_store(p.m_part + b, mo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(p.l_part + b, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __hip_atomic_store(orow + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       } else {
         if (d == 0) {
           p.m_part[b] = mo;
           p.l_part[b] = L;
         }
-        orow[d] = O;
+        *reinterpret_cast<fl4_t*>(orow) = O;  // o_part is 16-byte aligned and D a multiple of 4
       }
       // one split: the workgroup holds the whole result, so it writes the
       // output too and no merge follows (one launch per call)
-      if (p.S == 1) p.o[qh * D + d] = L > 0.0f ? (_Float16)(O / L) : (_Float16)0.0f;
+      if (p.S == 1) put_out();
     }
   }
 }
@@ -640,9 +689,9 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   constexpr int U = tiles_per_pass<FMT, D, HG, PAGED, PVV>();
   constexpr int VE = VG::VE;   // PV steps per tile
   constexpr int VD = VG::VD;   // dwords per V chunk
-  __shared__ float s_o[NW_MAX][HG][opitch<D>()];
-  __shared__ float s_m[HG][NW_MAX];
-  __shared__ float s_l[HG][NW_MAX];
+  __shared__ __attribute__((aligned(16))) float s_o[NW_MAX][HG][opitch<D>()];
+  __shared__ __attribute__((aligned(16))) float s_m[HG][NW_MAX];
+  __shared__ __attribute__((aligned(16))) float s_l[HG][NW_MAX];
   __shared__ __attribute__((aligned(16))) float s_mw[NW_MAX][64];  // in-kernel split merge
   __shared__ float s_mr[NW_MAX][65];
   __shared__ int s_last;
