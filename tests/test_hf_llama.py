@@ -507,9 +507,8 @@ def test_gpu_graphed_generation_quantized(fmt, monkeypatch):
     device-position quantizer and attended by the paged kernel with scale pages, in the captured
     step too. Replayed tokens equal the eager steps bit for bit, and the greedy tokens over the
     dynamic quantized cache (int8: a divergence only where that run's top-2 margin is below 2e-2;
-    int4 and fp8 are left out of that comparison, since a last-bit difference between two kernels
-    can move a later token across one of the quantizer's wide rounding steps and the greedy paths
-    apart; their per-step agreement is the test above)."""
+    int4 and fp8 are held to the measured account of their divergences in
+    test_gpu_quantized_greedy_paths_part_through_rounding_flips below)."""
     name = hf_llama.register()
     model = tiny_llama(dtype=torch.float16, device="cuda")
     set_impl(model, name)
@@ -539,6 +538,101 @@ def test_gpu_graphed_generation_quantized(fmt, monkeypatch):
         if a != b:
             assert margins[i] < 2e-2, ("divergence at step %d without a tie" % i, margins[i])
             break
+
+
+def _signed_codes(t, fmt):
+    """Codes as signed integers one quantizer step apart: int8 as is, int4 unpacked, fp8 e4m3 as
+    sign and magnitude of its bit pattern (adjacent values differ by one)."""
+    from fqkv_decode import quant
+
+    if fmt == "int4":
+        return quant.unpack_int4(t).to(torch.int16)
+    if fmt == "fp8":
+        b = t.view(torch.uint8).to(torch.int16)
+        return torch.where(b >= 128, -(b & 127), b)
+    return t.to(torch.int16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fmt", ["int8", "int4", "fp8"])
+def test_gpu_quantized_greedy_paths_part_through_rounding_flips(fmt):
+    """Why the greedy tokens over the dynamic and the static quantized cache may part (int4 at
+    step 23 of this prompt), measured by feeding the graphed path's 40 tokens to both caches:
+    (1) after the prompt both hold the same codes and scales, and the two kernels that read them
+    (strided for the dynamic cache, paged for the static one; different passes and split
+    choices) agree to their error bound but not bit for bit (over 20 random queries at least one
+    output element differs); (2) after the first decode step layer 0's new codes are still equal
+    (its inputs are the token's embedding) and every code that differs in a later layer is one
+    quantizer step from the other cache's, its scale equal or one fp16 ulp away: a last-bit
+    difference of the kernels moved a value across a rounding boundary; (3) the free-running
+    paths part exactly one token after the first step at which, fed the same tokens, the two
+    caches' logits rank a different token first (and never if no step does)."""
+    import fqkv_decode
+
+    name = hf_llama.register()
+    model = tiny_llama(dtype=torch.float16, device="cuda")
+    set_impl(model, name)
+    ids = torch.randint(0, 1000, (1, 45), generator=torch.Generator().manual_seed(8)).cuda()
+    L, steps = ids.shape[1], 40
+    graphed = hf_llama.generate_graphed(model, ids, steps, kv_format=fmt)[0].tolist()
+    dynamic, _ = greedy(model, ids, steps, hf_llama.QuantizedKVCache(model.config, fmt))
+    parted = next((i for i, (a, b) in enumerate(zip(dynamic, graphed)) if a != b), None)
+
+    qc = hf_llama.QuantizedKVCache(model.config, fmt)
+    sc = hf_llama.StaticKVCache(model.config, 128, fmt)
+    with torch.no_grad():
+        la = model(ids, past_key_values=qc, use_cache=True).logits[:, -1].float()
+        lb = model(ids, past_key_values=sc, use_cache=True).logits[:, -1].float()
+    assert torch.equal(la, lb)
+    for lq, ls in zip(qc.layers, sc.layers):
+        assert torch.equal(bits(lq._k[:, :, :L]), bits(ls.keys[:, :, :L]))
+        assert torch.equal(bits(lq._v[:, :, :L]), bits(ls.values[:, :, :L]))
+        assert torch.equal(lq._ks[:, :, :L], ls.key_scales[:, :, :L])
+        assert torch.equal(lq._vs[:, :, :L], ls.value_scales[:, :, :L])
+
+    # (1) the two kernels over layer 0's identical cache
+    lq, ls = qc.layers[0], sc.layers[0]
+    kq, vq = lq._views()
+    pages = lambda t: t.permute(0, 2, 1)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    differing, worst, scale = 0, 0.0, 0.0
+    for _ in range(20):
+        q = torch.randn(1, 8, 64, device="cuda", generator=g).half()
+        a = fqkv_decode.decode_attn_gqa_strided(q, kq, vq, 8, kq.fqkv_scales, vq.fqkv_scales)
+        b = fqkv_decode.decode_attn_gqa_paged(q, ls.keys.permute(0, 2, 1, 3), ls.values.permute(0, 2, 1, 3),
+                                              ls.page_table, ls.seq_lens, ls.keys.shape[2], 8,
+                                              pages(ls.key_scales), pages(ls.value_scales))
+        d = (a.float() - b.float()).abs()
+        differing += int((d > 0).sum())
+        worst = max(worst, float(d.max()))
+        scale = max(scale, float(a.float().abs().max()))
+    assert differing > 0 and worst <= 4e-3 * max(1.0, scale), (differing, worst, scale)
+
+    # (2) and (3): the graphed path's tokens fed to both caches
+    first_rank = None
+    with torch.no_grad():
+        for t in range(steps):
+            tok = torch.tensor([[graphed[t]]], device="cuda")
+            la = model(tok, past_key_values=qc, use_cache=True).logits[:, -1].float()
+            lb = model(tok, past_key_values=sc, position_ids=torch.tensor([[L + t]], device="cuda"),
+                       use_cache=True).logits[:, -1].float()
+            if first_rank is None and int(la.argmax()) != int(lb.argmax()):
+                first_rank = t
+            if t == 0:
+                for i, (lq, ls) in enumerate(zip(qc.layers, sc.layers)):
+                    for cq, cs, sq, ss in ((lq._k, ls.keys, lq._ks, ls.key_scales),
+                                           (lq._v, ls.values, lq._vs, ls.value_scales)):
+                        x = _signed_codes(cq[:, :, L:L + 1], fmt)
+                        y = _signed_codes(cs[:, :, L:L + 1], fmt)
+                        su = (sq[:, :, L:L + 1].view(torch.int16).int() - ss[:, :, L:L + 1].view(torch.int16).int()).abs()
+                        if i == 0:
+                            assert torch.equal(x, y) and int(su.max()) == 0
+                        else:
+                            assert int((x - y).abs().max()) <= 1 and int(su.max()) <= 1
+    if parted is None:
+        assert first_rank is None or first_rank == steps - 1
+    else:
+        assert first_rank == parted - 1, (first_rank, parted)
 
 
 @pytest.mark.gpu
