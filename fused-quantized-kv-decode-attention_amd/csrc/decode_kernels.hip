@@ -674,19 +674,25 @@ __device__ __forceinline__ void pin_sgprs(const PartialParams& p) {
 // 100.6 -> 95.7 us, B 256 19.2 -> 17.4 us. Measured slower, and kept at four:
 // int4 at D 128 (B 256 +14 %), int8 at D 64 (B 256 +12 %), sixteen tiles for
 // int4 (B 2048 +8 % at D 64; 2 waves per SIMD), and the paged rows (2 waves).
-template <int FMT, int D, int HG, bool PAGED, bool PVV>
+// SHORT: two tiles (the fewest the paired P.V products take), for fp16 / bf16
+// splits of at most two tiles per wave, where a four-tile pass issues loads,
+// address arithmetic and products for tiles past the split's end: D 128,
+// batch 1, N 512 / 1024 / 2048 5.54 -> 5.22, 5.82 -> 5.57, 6.80 -> 6.18 us,
+// N 1 3.57 -> 3.16 us (same-box A/B).
+template <int FMT, int D, int HG, bool PAGED, bool PVV, bool SHORT = false>
 constexpr int tiles_per_pass() {
-  return (FMT == KV_I4 && D == 64 && HG == 1 && !PAGED && !PVV) ? 8 : 4;
+  return SHORT ? 2 : ((FMT == KV_I4 && D == 64 && HG == 1 && !PAGED && !PVV) ? 8 : 4);
 }
 
 // KEEPV: int4 rows token-major without pages (heads sharing cache lines, the
 // launcher's head grouping on), whose V loads go without the non-temporal hint.
-template <int FMT, int D, int HG, bool PAGED, bool PVV = false, bool KEEPV = false>
+template <int FMT, int D, int HG, bool PAGED, bool PVV = false, bool KEEPV = false, bool SHORT = false>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
   static_assert(!PVV || (FMT == KV_F16 && !PAGED), "P.V on the vector ALUs: fp16, contiguous rows");
   using VG = VGeom<F::ROWB, D>;
-  constexpr int U = tiles_per_pass<FMT, D, HG, PAGED, PVV>();
+  static_assert(!SHORT || ((FMT == KV_F16 || FMT == KV_BF16) && !PAGED && !PVV && !KEEPV), "short passes: fp16 / bf16 rows");
+  constexpr int U = tiles_per_pass<FMT, D, HG, PAGED, PVV, SHORT>();
   constexpr int VE = VG::VE;   // PV steps per tile
   constexpr int VD = VG::VD;   // dwords per V chunk
   __shared__ __attribute__((aligned(16))) float s_o[NW_MAX][HG][opitch<D>()];
@@ -1490,6 +1496,14 @@ static hipError_t launch_partial_t(const PartialParams& p, int nblocks, int nw, 
     if (!p.page_table && g_pv_valu.load(std::memory_order_relaxed)) {
       lds += (size_t)nw * tiles_per_pass<FMT, D, HG, false, true>() * 16 * HG * sizeof(float);
       hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false, true>), dim3(nblocks), dim3(64 * nw), lds, st, p);
+      return hipGetLastError();
+    }
+  }
+  if constexpr (FMT == KV_F16 || FMT == KV_BF16) {
+    // at most two tiles per wave: two-tile passes
+    if (!p.page_table && (p.chunk + 15) / 16 <= 2 * nw) {
+      hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false, false, false, true>), dim3(nblocks), dim3(64 * nw),
+                         lds, st, p);
       return hipGetLastError();
     }
   }
