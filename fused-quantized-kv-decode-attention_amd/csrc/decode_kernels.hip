@@ -674,11 +674,14 @@ __device__ __forceinline__ void pin_sgprs(const PartialParams& p) {
 // 100.6 -> 95.7 us, B 256 19.2 -> 17.4 us. Measured slower, and kept at four:
 // int4 at D 128 (B 256 +14 %), int8 at D 64 (B 256 +12 %), sixteen tiles for
 // int4 (B 2048 +8 % at D 64; 2 waves per SIMD), and the paged rows (2 waves).
-// SHORT: two tiles (the fewest the paired P.V products take), for fp16 / bf16
-// splits of at most two tiles per wave, where a four-tile pass issues loads,
-// address arithmetic and products for tiles past the split's end: D 128,
-// batch 1, N 512 / 1024 / 2048 5.54 -> 5.22, 5.82 -> 5.57, 6.80 -> 6.18 us,
-// N 1 3.57 -> 3.16 us (same-box A/B).
+// SHORT: two tiles (the fewest the paired P.V products take), for splits of
+// at most two tiles per wave on contiguous rows, where a four-tile pass issues
+// loads, address arithmetic and products for tiles past the split's end.
+// Same-box A/B, split-K D 128, batch 1: fp16 at N 512 / 2048 / 4096 / 8192
+// 5.55 -> 5.24, 6.81 -> 6.20, 8.31 -> 7.36, 10.01 -> 9.33 us; int8 6.62 ->
+// 6.00, 7.14 -> 6.50, 8.56 -> 7.56, 9.02 -> 8.28 us; int4 6.30 -> 5.77,
+// 6.57 -> 6.01, 7.65 -> 6.94, 7.85 -> 6.99 us; N 16384 (four tiles per wave,
+// the usual pass) unchanged.
 template <int FMT, int D, int HG, bool PAGED, bool PVV, bool SHORT = false>
 constexpr int tiles_per_pass() {
   return SHORT ? 2 : ((FMT == KV_I4 && D == 64 && HG == 1 && !PAGED && !PVV) ? 8 : 4);
@@ -691,7 +694,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   using F = Fmt<FMT, D>;
   static_assert(!PVV || (FMT == KV_F16 && !PAGED), "P.V on the vector ALUs: fp16, contiguous rows");
   using VG = VGeom<F::ROWB, D>;
-  static_assert(!SHORT || ((FMT == KV_F16 || FMT == KV_BF16) && !PAGED && !PVV && !KEEPV), "short passes: fp16 / bf16 rows");
+  static_assert(!SHORT || (!PAGED && !PVV && !KEEPV), "short passes: contiguous rows");
   constexpr int U = tiles_per_pass<FMT, D, HG, PAGED, PVV, SHORT>();
   constexpr int VE = VG::VE;   // PV steps per tile
   constexpr int VD = VG::VD;   // dwords per V chunk
@@ -1499,9 +1502,9 @@ static hipError_t launch_partial_t(const PartialParams& p, int nblocks, int nw, 
       return hipGetLastError();
     }
   }
-  if constexpr (FMT == KV_F16 || FMT == KV_BF16) {
+  {
     // at most two tiles per wave: two-tile passes
-    if (!p.page_table && (p.chunk + 15) / 16 <= 2 * nw) {
+    if (!p.page_table && !(FMT == KV_I4 && p.hg_k) && (p.chunk + 15) / 16 <= 2 * nw) {
       hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false, false, false, true>), dim3(nblocks), dim3(64 * nw),
                          lds, st, p);
       return hipGetLastError();
