@@ -689,12 +689,18 @@ constexpr int tiles_per_pass() {
 
 // KEEPV: int4 rows token-major without pages (heads sharing cache lines, the
 // launcher's head grouping on), whose V loads go without the non-temporal hint.
-template <int FMT, int D, int HG, bool PAGED, bool PVV = false, bool KEEPV = false, bool SHORT = false>
+// LAZY (int8 / int4 / fp8 / bf16, each wave one four-tile pass): the query's
+// derived operands are formed, and a pass's scales unpacked, only once the
+// pass's K and V loads are all out (see qprep and the scale loads below);
+// with several passes per wave the registers this keeps live cost occupancy.
+template <int FMT, int D, int HG, bool PAGED, bool PVV = false, bool KEEPV = false, bool SHORT = false,
+          bool LAZY = false>
 __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialParams p) {
   using F = Fmt<FMT, D>;
   static_assert(!PVV || (FMT == KV_F16 && !PAGED), "P.V on the vector ALUs: fp16, contiguous rows");
   using VG = VGeom<F::ROWB, D>;
   static_assert(!SHORT || (!PAGED && !PVV && !KEEPV), "short passes: contiguous rows");
+  static_assert(!LAZY || (!PAGED && !PVV && !KEEPV), "lazy preparation: contiguous rows");
   constexpr int U = tiles_per_pass<FMT, D, HG, PAGED, PVV, SHORT>();
   constexpr int VE = VG::VE;   // PV steps per tile
   constexpr int VD = VG::VD;   // dwords per V chunk
@@ -774,30 +780,40 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     for (int i = 0; i < F::NKI; ++i) qb[i] = F::qfrag(rQ, qrow * D, i, R);
   }
   // bf16 products take the fp16 query as two bf16 operands, q = hi + lo
-  // exactly (hi holds 8 of q's 11 significant bits, lo the rest)
+  // exactly (hi holds 8 of q's 11 significant bits, lo the rest); int8 / int4
+  // scores come out of the matrix cores as 2^-24 (q.k + BIAS sum(q)) over the
+  // query as the operands carry it, qbias = BIAS sum(q) of the lane's column
+  // (zero for fp16). Both need the query's values: formed here, the wait for
+  // the query puts a memory round trip ahead of the first K load, so LAZY
+  // forms them in the first pass once its K / V loads are out (same-box A/B:
+  // int8 / int4 MHA at B 8, N 4096, D 128 6.59 -> 6.10 / 5.81 -> 5.36 us, at
+  // B 32, N 512 6.39 -> 6.07 / 6.06 -> 5.67 us; split-K at N 16384 10.97 ->
+  // 10.83 / 8.68 -> 8.51 us; B 256 and 2048, several passes a wave: eager).
   bf8_t qhi[F::BF16 ? F::NKI : 1], qlo[F::BF16 ? F::NKI : 1];
-  if constexpr (F::BF16) {
-#pragma unroll
-    for (int i = 0; i < F::NKI; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float f = (float)qb[i][e];
-        qhi[i][e] = (__bf16)f;
-        qlo[i][e] = (__bf16)(f - (float)qhi[i][e]);
-      }
-  }
-  // int8 / int4 scores come out of the matrix cores as 2^-24 (q.k + BIAS
-  // sum(q)) over the query as the operands carry it; qbias = BIAS sum(q) of
-  // the lane's column (zero for fp16)
   float qbias = 0.0f;
-  if constexpr (F::BIASED) {
-    float qs = 0.0f;
+  constexpr bool QPREP = F::BF16 || F::BIASED;
+  bool qready = !LAZY;
+  auto qprep = [&]() {
+    if constexpr (F::BF16) {
 #pragma unroll
-    for (int i = 0; i < F::NKI; ++i)
+      for (int i = 0; i < F::NKI; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qs += (float)qb[i][e] * (16777216.0f / F::kunit(e));
-    qbias = F::BIAS * rows4_sum(qs);
-  }
+        for (int e = 0; e < 8; ++e) {
+          const float f = (float)qb[i][e];
+          qhi[i][e] = (__bf16)f;
+          qlo[i][e] = (__bf16)(f - (float)qhi[i][e]);
+        }
+    }
+    if constexpr (F::BIASED) {
+      float qs = 0.0f;
+#pragma unroll
+      for (int i = 0; i < F::NKI; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qs += (float)qb[i][e] * (16777216.0f / F::kunit(e));
+      qbias = F::BIAS * rows4_sum(qs);
+    }
+  };
+  if constexpr (QPREP && !LAZY) qprep();
 
   float m_run = -INFINITY, l_run = 0.0f;  // of column n, over the tokens this lane scored
   float w_run = 0.0f;  // int8 / int4: sum of the lane's PV weights, in acc's units
@@ -911,19 +927,29 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       else
         F::load_k(src[u].k, koff + (F::SOFF_TILE ? 0u : src[u].off), kr[u], F::SOFF_TILE ? src[u].off : 0u);
     }
+    // contiguous rows: with LAZY the scale loads' raw dwords, unpacked once
+    // the V loads are out too (unpacked here, a pass waits for its K loads and
+    // scales before its V loads leave)
+    const bool vec_now = vec_sc && full;  // wave-uniform
+    u2_t ksa[F::QUANT && !PAGED && LAZY ? NG : 1], vsa[F::QUANT && !PAGED && LAZY ? NG : 1];
     if constexpr (F::QUANT) {
       if constexpr (!PAGED) {
-        if (vec_sc && full) {
+        if (vec_now) {
 #pragma unroll
           for (int g = 0; g < NG; ++g) {
             const uint32_t so = (uint32_t)(pb + g * P * step) * 2u;  // wave-uniform
             const uint32_t vo = (uint32_t)lane_tok * 2u + (F::SOFF_TILE ? 0u : so);
-            const u2_t a = buf_load<8>(rKs, vo, F::SOFF_TILE ? so : 0u);
-            const u2_t c = buf_load<8>(rVs, vo, F::SOFF_TILE ? so : 0u);
+            if constexpr (LAZY) {
+              ksa[g] = buf_load<8>(rKs, vo, F::SOFF_TILE ? so : 0u);
+              vsa[g] = buf_load<8>(rVs, vo, F::SOFF_TILE ? so : 0u);
+            } else {
+              const u2_t a = buf_load<8>(rKs, vo, F::SOFF_TILE ? so : 0u);
+              const u2_t c = buf_load<8>(rVs, vo, F::SOFF_TILE ? so : 0u);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              ks[g][k] = __builtin_bit_cast(_Float16, (uint16_t)(a[k / 2] >> (16 * (k % 2))));
-              vs[g][k] = __builtin_bit_cast(_Float16, (uint16_t)(c[k / 2] >> (16 * (k % 2))));
+              for (int k = 0; k < 4; ++k) {
+                ks[g][k] = __builtin_bit_cast(_Float16, (uint16_t)(a[k / 2] >> (16 * (k % 2))));
+                vs[g][k] = __builtin_bit_cast(_Float16, (uint16_t)(c[k / 2] >> (16 * (k % 2))));
+              }
             }
           }
         } else {
@@ -976,6 +1002,24 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
     }
     __builtin_amdgcn_sched_barrier(0);  // keep every load of the pass ahead of its use
     FQKV_STAMP(1);  // every load of the pass issued
+    if constexpr (QPREP && LAZY) {
+      if (!qready) {
+        qprep();
+        qready = true;
+      }
+    }
+    if constexpr (F::QUANT && !PAGED && LAZY) {
+      if (vec_now) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            const uint32_t a = ksa[g][k / 2], c = vsa[g][k / 2];
+            ks[g][k] = __builtin_bit_cast(_Float16, (uint16_t)(a >> (16 * (k % 2))));
+            vs[g][k] = __builtin_bit_cast(_Float16, (uint16_t)(c >> (16 * (k % 2))));
+          }
+      }
+    }
 
     if constexpr (PICK_SC) {
 #pragma unroll
@@ -1502,11 +1546,21 @@ static hipError_t launch_partial_t(const PartialParams& p, int nblocks, int nw, 
       return hipGetLastError();
     }
   }
-  {
+  // the formats with query operands or scales to prepare: LAZY when every wave
+  // has one four-tile pass (with two-tile passes it measured slower: int8 /
+  // int4 split-K at N 4096 +0.27 us, where N 512 gained 0 / 0.25 us)
+  constexpr bool LZ = Fmt<FMT, D>::QUANT || FMT == KV_BF16;
+  const int tiles = (p.chunk + 15) / 16;
+  if (!p.page_table && !(FMT == KV_I4 && p.hg_k)) {
     // at most two tiles per wave: two-tile passes
-    if (!p.page_table && !(FMT == KV_I4 && p.hg_k) && (p.chunk + 15) / 16 <= 2 * nw) {
-      hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false, false, false, true>), dim3(nblocks), dim3(64 * nw),
-                         lds, st, p);
+    if (tiles <= 2 * nw) {
+      hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false, false, false, true>), dim3(nblocks),
+                         dim3(64 * nw), lds, st, p);
+      return hipGetLastError();
+    }
+    if (LZ && tiles <= tiles_per_pass<FMT, D, HG, false, false>() * nw) {
+      hipLaunchKernelGGL((decode_partial_kernel<FMT, D, HG, false, false, false, false, LZ>), dim3(nblocks),
+                         dim3(64 * nw), lds, st, p);
       return hipGetLastError();
     }
   }
