@@ -131,6 +131,31 @@ def gate(torch, fq, q, K, V, S, W, CW):
 # Python, half a microsecond per call when only 20 calls are timed). They lie outside the region.
 LEAD_CALLS = 4
 
+# A loop timed within ~0.25 s of allocating fresh device memory (multi-GB inputs through PyTorch's
+# caching allocator) reads 3-5 % slow on MI355X, and a plain 1 GiB streaming read does too; 0.25 s
+# later the same loop on the same buffers is back to its steady rate (int4 MHA B 2048, N 4096,
+# D 128: 176 -> 169 us; headline 14.5 -> 13.9 us after a 4 GB allocation). So every timed row
+# lets SETTLE_S pass between allocating its inputs and its warm-up calls. The headline waits idle
+# (its warm-up is the --warmup count alone); the other rows, whose warm-up is this file's choice,
+# spend the time launching the streaming-read probe over a 32 MiB buffer, since after an idle wait
+# the clocks are down and a host-bound loop of small calls (GQA B 1, N 512) reads up to 45 % slow.
+SETTLE_S = 0.4
+_SETTLE_BUF = []
+
+
+def settle(torch, fq=None):
+    torch.cuda.synchronize()
+    if fq is None:
+        time.sleep(SETTLE_S)
+        return
+    if not _SETTLE_BUF:
+        _SETTLE_BUF.append(torch.ones(32 << 20, dtype=torch.uint8, device="cuda"))
+    t_end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < t_end:
+        for _ in range(100):
+            fq._ext._probe_stream_read(_SETTLE_BUF[0], 256)
+        torch.cuda.synchronize()
+
 
 def time_calls(torch, fq, q, Ks, Vs, S, W, CW, steps, warmup):
     mp = torch.empty(HQ, S, device="cuda")
@@ -253,6 +278,7 @@ def stream_ceiling(torch, fq, steps, warmup, nsets=10):
     workgroups of 256 threads)."""
     nb = 4 * HKV * N * D
     bufs = [torch.full((nb,), 1, dtype=torch.uint8, device="cuda") for _ in range(nsets)]
+    settle(torch, fq)
     best = None
     for blocks in (256, 512, 1024):
         ms = _loop_ms(torch, lambda i: fq._ext._probe_stream_read(bufs[i], blocks), nsets, steps, warmup)
@@ -314,6 +340,7 @@ def secondary_results(torch, fq, steps=400, warmup=50):
         err = float((fn()[rows].float() - _ref_mha(torch, q[rows], Kf, Vf)).abs().max())
         if err > 2e-3:
             raise RuntimeError("secondary gate failed: MHA %s B=2048 max-abs %.3e" % (fmt, err))
+        settle(torch, fq)
         ms = _loop_ms(torch, lambda i: fn(), 1, steps, warmup)
         mha[fmt] = {"us_per_call": round(ms * 1e3, 2), "GBps": round(nbytes / ms / 1e6, 1), "frac": _frac(nbytes, ms),
                     "alg_bytes": nbytes, "gate_max_abs_err": err}
@@ -335,6 +362,7 @@ def secondary_results(torch, fq, steps=400, warmup=50):
     ref = _ref_mha(torch, qs[heads], Ksk[kv_rows].float().repeat_interleave(G, 0),
                    Vsk[kv_rows].float().repeat_interleave(G, 0))
     nbytes = Bs * (4 * Hkv * Ns * Ds + 4 * Hq * Ds)
+    settle(torch, fq)
     best = None
     for S in (4, 8, 16):
         for Wk in (4, 8):
@@ -480,6 +508,7 @@ def suite_mha_quant(torch, fq, steps, warmup, rows, shapes=None, formats=("fp16"
             ref = _ref_mha(torch, q, Kf, Vf)
             err = float((o.float() - ref).abs().max())
             del Kf, Vf, ref
+            settle(torch, fq)
             ms = _loop_ms(torch, fn, ns, steps, warmup)
             extra = {}
             if Dm == 64 and fmt != "fp8":
@@ -517,6 +546,7 @@ def suite_gqa(torch, fq, steps, warmup, rows, shapes=None):
         o = fq.decode_attn_gqa(q, K0, V0, W)
         err = float((o.reshape(B * Hq, Dg).float() - ref).abs().max())
         nbytes = B * (4 * Hkv * N * Dg + 4 * Hq * Dg)
+        settle(torch, fq)
         ms = _loop_ms(torch, lambda i: fq.decode_attn_gqa(q, sets[i][0], sets[i][1], W), ns, steps, warmup)
         qf = q.reshape(B * Hq, Dg)
 
@@ -552,6 +582,7 @@ def suite_splitk(torch, fq, steps, warmup, rows):
         K0, V0 = sets[0]
         ref = _ref_mha(torch, q, K0.float().repeat_interleave(G, 0), V0.float().repeat_interleave(G, 0))
         nbytes = B * (4 * Hkv * N * Dd + 4 * Hq * Dd)
+        settle(torch, fq)
         best = None
         for S in (1, 2, 4, 8, 16, 32, 64, 128):
             if S > max(1, N // 16):
@@ -594,6 +625,7 @@ def suite_mha_small(torch, fq, steps, warmup, rows):
     o = fq.decode_attn_fp16_mw(q, sets[0][0], sets[0][1], W)
     err = float((o.float() - _ref_mha(torch, q, sets[0][0].float(), sets[0][1].float())).abs().max())
     nbytes = B * (4 * N * Dm + 4 * Dm)
+    settle(torch, fq)
     ms = _loop_ms(torch, lambda i: fq.decode_attn_fp16_mw(q, sets[i][0], sets[i][1], W), ns, steps, warmup)
     rows.append(_row("mha_fp16", {"B": B, "N": N, "D": Dm, "W": W, "sets": ns}, ms, nbytes, err))
     log("mha_fp16  B=%d N=%d D=%d  %8.2f us  %7.1f GB/s  err %.2e" % (B, N, Dm, ms * 1e3, nbytes / ms / 1e6, err))
@@ -626,6 +658,7 @@ def suite_splitk_quant(torch, fq, steps, warmup, rows, cases=((1, 16384), (8, 32
             del Kf, Vf
             f = {"int8": fq.gqa_sk_fast_int8, "int4": fq.gqa_sk_fast_int4, "fp8": fq.gqa_sk_fast_fp8}[fmt]
             nbytes = B * ((Hkv * N * Dd if fmt == "int4" else 2 * Hkv * N * Dd) + 4 * Hkv * N + 4 * Hq * Dd)
+            settle(torch, fq)
             best = None
             for S in ((16, 32, 64) if B == 1 else (4, 8, 16)):
                 for W in (4, 8):
@@ -692,6 +725,7 @@ def suite_paged(torch, fq, steps, warmup, rows):
         nbytes = B * (kvb + 4 * Hq * Dd)
         o = contiguous()
         err = float((o[0].float() - ref0).abs().max())
+        settle(torch, fq)
         ms = _loop_ms(torch, lambda i: contiguous(), 1, nsteps, nwarm)
         cfg = {"B": B, "Hq": Hq, "Hkv": Hkv, "N": N, "D": Dd, "W": W, "fmt": fmt}
         rows.append(_row("gqa_contiguous_" + fmt, cfg, ms, nbytes, err))
@@ -704,6 +738,7 @@ def suite_paged(torch, fq, steps, warmup, rows):
         on = fn(0)
         nerr = float((on[0].float() - ref0).abs().max())
         same = bool(torch.equal(on, o))
+        settle(torch, fq)
         ms = _loop_ms(torch, fn, 1, nsteps, nwarm)
         rows.append(_row("gqa_nhd_" + fmt, cfg, ms, nbytes, nerr, equal_to_contiguous=same))
         log("paged suite: token-major %s       %8.2f us  %7.1f GB/s  err %.2e  equal to contiguous: %s"
@@ -734,6 +769,7 @@ def suite_paged(torch, fq, steps, warmup, rows):
             perr = float((op[0].float() - ref0).abs().max())
             same = bool(torch.equal(op, o))
             pb = nbytes + B * npb * 4
+            settle(torch, fq)
             ms = _loop_ms(torch, fn, 1, nsteps, nwarm)
             lay = "HND" if hnd else "NHD"
             rows.append(_row("gqa_paged_" + fmt, dict(cfg, page=page, pages=lay), ms, pb, perr,
@@ -766,6 +802,7 @@ def suite_quant(torch, fq, steps, warmup, rows):
                 continue
             elems = rows_ * N_ * Dd
             nbytes = elems * X.element_size() + (elems if fmt == "int8" else elems // 2) + 2 * rows_ * N_
+            settle(torch, fq)
             ms = _loop_ms(torch, lambda i: f(X), 1, max(50, steps // 4), max(10, warmup // 4))
             rows.append(_row("quantize_" + fmt, {"rows": rows_ * N_, "D": Dd, "src": src}, ms, nbytes,
                              equal_to_torch_expressions=same))
@@ -1145,6 +1182,7 @@ def splitk_primary_table(torch, fq, sweep_steps=200, sweep_warmup=20, steps=2000
             ref = _ref_mha(torch, q, sets[0][0].float().repeat_interleave(G, 0),
                            sets[0][1].float().repeat_interleave(G, 0))
             nbytes = alg_bytes(n=Nn, d=Dd)
+            settle(torch, fq)
             best = None
             for S in (8, 16, 32, 64, 128):
                 if S > Nn // 16:
@@ -1398,6 +1436,7 @@ def main():
         print(json.dumps(res), flush=True)
         return
 
+    settle(torch)
     ms = time_calls(torch, fq, q, Ks, Vs, S, W, CW, args.steps, args.warmup)
     ms_long = time_calls(torch, fq, q, Ks, Vs, S, W, CW, 2000, 200) if args.steps < 2000 else ms
     ev = HipEvents()

@@ -74,10 +74,18 @@ constexpr float LOG2E = 1.4426950408889634f;
 #ifdef FQKV_TIMELINE
 constexpr int TIMELINE_BLOCKS = 4096;
 __device__ unsigned long long g_timeline[TIMELINE_BLOCKS][NW_MAX][16];
+// The stamp takes its own copy of the workgroup id (an asm move the compiler
+// cannot merge with the kernel's uses): indexing g_timeline with blockIdx.x
+// itself under the lane-0 branch made the compiler carry the id in a vector
+// register through the branch and reuse that copy in the kernel's index
+// math, so every buffer descriptor built from it became per-lane and each
+// buffer load a readfirstlane loop over the wave.
 #define FQKV_STAMP(stage)                                                                          \
   do {                                                                                             \
-    if ((threadIdx.x & 63) == 0 && blockIdx.x < TIMELINE_BLOCKS)                                   \
-      g_timeline[blockIdx.x][threadIdx.x >> 6][stage] = __builtin_amdgcn_s_memrealtime();          \
+    uint32_t blk_;                                                                                 \
+    asm volatile("s_mov_b32 %0, %1" : "=s"(blk_) : "s"(blockIdx.x));                              \
+    const unsigned long long t_ = __builtin_amdgcn_s_memrealtime();                                \
+    if ((threadIdx.x & 63) == 0 && blk_ < TIMELINE_BLOCKS) g_timeline[blk_][threadIdx.x >> 6][stage] = t_; \
   } while (0)
 extern "C" int fqkv_timeline_read(void* host, size_t bytes) {
   if (bytes == (size_t)-1) {
