@@ -277,11 +277,17 @@ int run_decode(int fmt, const void* q, const void* K, const void* V, const void*
     p.o_part = f + acc_offset_floats(heads, S);
     p.slot = merge_slot(st, rows * ngroups, &p.xcd_ok);
   }
-  // With four or more work items per CU, workgroups of 4 waves: several
-  // share a CU and hide each other's memory latency (measured on MI355X, MHA
-  // at N 4096: never slower than 8 waves from batch 1024 on, 5-12 % faster
-  // for int4 / int8 at D 128 and fp16 at D 64). W is a maximum.
-  const int64_t nw = (nblocks >= 4LL * cus && W > 4) ? 4 : W;
+  // Workgroups of 4 waves with four times as many work items as CUs, and
+  // with more unsplit work items than CUs for rows under 256 bytes: several
+  // share a CU and hide each other's memory latency, where 8-wave ones fit
+  // one per CU at these kernels' register counts and leave a partial round
+  // (same-box A/B on MI355X at N 4096, 384 / 512 / 768 KV rows: int8 at
+  // D 128 -9 / -8 / -6 %, int4 -11 / -9 / -9 %, fp8 and int8 at D 64 -8 to
+  // -13 %, fp16 at D 64 -13 / -3 / -6 %, int4 at D 64 within 3 %; fp16 /
+  // bf16 rows of 256 bytes run 1-2 % slower with 4 waves there and keep 8
+  // below 4 x CUs). W is a maximum.
+  const bool many = nblocks >= 4LL * cus || (S == 1 && nblocks > cus && row_bytes_of(fmt, D) < 256);
+  const int64_t nw = (many && W > 4) ? 4 : W;
   int xcd_local = 0;
   hipError_t e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)nw, st, &xcd_local);
   if (e != hipSuccess) return hip_fail(e, "launch: partial kernel");
