@@ -278,15 +278,19 @@ int run_decode(int fmt, const void* q, const void* K, const void* V, const void*
     p.slot = merge_slot(st, rows * ngroups, &p.xcd_ok);
   }
   // Workgroups of 4 waves with four times as many work items as CUs, and
-  // with more unsplit work items than CUs for rows under 256 bytes: several
-  // share a CU and hide each other's memory latency, where 8-wave ones fit
-  // one per CU at these kernels' register counts and leave a partial round
-  // (same-box A/B on MI355X at N 4096, 384 / 512 / 768 KV rows: int8 at
-  // D 128 -9 / -8 / -6 %, int4 -11 / -9 / -9 %, fp8 and int8 at D 64 -8 to
-  // -13 %, fp16 at D 64 -13 / -3 / -6 %, int4 at D 64 within 3 %; fp16 /
-  // bf16 rows of 256 bytes run 1-2 % slower with 4 waves there and keep 8
+  // with more unsplit work items than CUs for rows under 256 bytes (128-byte
+  // rows from one per CU on): several share a CU and hide each other's
+  // memory latency, where 8-wave ones fit one per CU at these kernels'
+  // register counts and leave a partial round (same-box A/B on MI355X at
+  // N 4096, 384 / 512 / 768 KV rows: int8 at D 128 -9 / -8 / -6 %, int4
+  // -11 / -9 / -9 %, fp8 and int8 at D 64 -8 to -13 %, fp16 at D 64 -13 /
+  // -3 / -6 %, int4 at D 64 within 3 %; at 256 rows int8 / fp8 at D 128 and
+  // fp16 at D 64 -6 to -8 %, while 64-byte rows are faster with 8 waves;
+  // fp16 / bf16 rows of 256 bytes run 1-2 % slower with 4 waves and keep 8
   // below 4 x CUs). W is a maximum.
-  const bool many = nblocks >= 4LL * cus || (S == 1 && nblocks > cus && row_bytes_of(fmt, D) < 256);
+  const int64_t rowb = row_bytes_of(fmt, D);
+  const bool many = nblocks >= 4LL * cus ||
+                    (S == 1 && rowb < 256 && (nblocks > cus || (rowb == 128 && nblocks == cus)));
   const int64_t nw = (many && W > 4) ? 4 : W;
   int xcd_local = 0;
   hipError_t e = launch_partial(fmt, (int)D, hg, p, (int)nblocks, (int)nw, st, &xcd_local);
