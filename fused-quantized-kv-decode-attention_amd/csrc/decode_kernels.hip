@@ -566,8 +566,15 @@ __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const f
     const int h = idx / D;
     const int d = idx - h * D;
     float mw[NWC], lw[NWC];
+    fl4_t a[NWC];
     lds_row<NWC>(s_m[h], mw);
     lds_row<NWC>(s_l[h], lw);
+#pragma unroll
+    for (int ww = 0; ww < NWC; ++ww) a[ww] = *reinterpret_cast<const fl4_t*>(&s_o[ww][h][d]);
+    // every LDS read of the merge in flight before the first use: left to
+    // itself the compiler issued the waves' acc rows one or two at a time,
+    // behind the maximum and the weights, a chain of LDS round trips
+    __builtin_amdgcn_sched_barrier(0);
     float M = mw[0];
 #pragma unroll
     for (int j = 1; j < NWC; ++j) M = fmaxf(M, mw[j]);
@@ -582,11 +589,10 @@ __device__ __forceinline__ void merge_waves_emit(const PartialParams& p, const f
     fl4_t O = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int ww = 0; ww < NWC; ++ww) {
-      const fl4_t a = *reinterpret_cast<const fl4_t*>(&s_o[ww][h][d]);
-      O.x = fmaf(wj[ww], a.x, O.x);
-      O.y = fmaf(wj[ww], a.y, O.y);
-      O.z = fmaf(wj[ww], a.z, O.z);
-      O.w = fmaf(wj[ww], a.w, O.w);
+      O.x = fmaf(wj[ww], a[ww].x, O.x);
+      O.y = fmaf(wj[ww], a[ww].y, O.y);
+      O.z = fmaf(wj[ww], a[ww].z, O.z);
+      O.w = fmaf(wj[ww], a[ww].w, O.w);
     }
     const size_t qh = qrow0 + h;
     // normalised fp16 output (an empty sequence gives zeros)
