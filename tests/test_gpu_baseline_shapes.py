@@ -151,3 +151,38 @@ def test_gqa_split_k_batch8_n32k(S, W, merge_mode):
     ref_rows = oracle.gqa_attention(q[heads].cpu().numpy().reshape(1, -1, D),
                                     K[kv_rows].cpu().numpy()[None], V[kv_rows].cpu().numpy()[None])[0]
     check(o, ref_full, ref_rows, heads)
+
+
+@pytest.mark.parametrize("fmt,D", [("fp16", 64), ("fp16", 128), ("int8", 128), ("int8", 64), ("int4", 128), ("int4", 64)])
+@pytest.mark.parametrize("per_cu", [1.5, 3.0])
+def test_mha_rows_between_one_and_four_per_cu(fmt, D, per_cu):
+    """Unsplit calls with more rows than CUs but fewer than four per CU: rows under
+    256 bytes run 4-wave workgroups there, 256-byte rows 8-wave ones (the
+    single-block entry points' wave-count rule); both against the references."""
+    B = int(per_cu * fq.cu_count())
+    N, W = 1024, 8
+    g = torch.Generator(device=DEV).manual_seed(B + D)
+    q = torch.randn(B, D, device=DEV, generator=g).half()
+    rows = sample_rows(B, seed=B + D)
+    if fmt == "fp16":
+        K = torch.randn(B, N, D, device=DEV, generator=g).half()
+        V = torch.randn(B, N, D, device=DEV, generator=g).half()
+        out = fq.decode_attn_fp16_mw(q, K, V, W)
+        ref_full = ref_fp32(q, K.float(), V.float())
+        Kr, Vr = K[rows].float().cpu().numpy(), V[rows].float().cpu().numpy()
+    else:
+        quantize = fq.quantize_int8_per_token if fmt == "int8" else fq.quantize_int4_per_token
+        Kq, Ks = quantize(torch.randn(B, N, D, device=DEV, generator=g))
+        Vq, Vs = quantize(torch.randn(B, N, D, device=DEV, generator=g))
+        if fmt == "int8":
+            out = fq.decode_attn_int8_mw(q, Kq, Vq, Ks, Vs, W)
+            deq, deq_gpu = oracle.dequant_int8, (lambda x, s: x.float() * s.float()[..., None])
+        else:
+            from fqkv_decode import quant
+            out = fq.decode_attn_int4(q, Kq, Vq, Ks, Vs, W)
+            deq, deq_gpu = oracle.dequant_int4, quant.dequant_int4
+        ref_full = ref_fp32(q, deq_gpu(Kq, Ks), deq_gpu(Vq, Vs))
+        Kr = deq(Kq[rows].cpu().numpy(), Ks[rows].cpu().numpy())
+        Vr = deq(Vq[rows].cpu().numpy(), Vs[rows].cpu().numpy())
+    assert out.shape == (B, D) and out.dtype == torch.float16
+    check(out, ref_full, oracle.attention(q[rows].cpu().numpy(), Kr, Vr), rows)
