@@ -137,7 +137,8 @@ LEAD_CALLS = 4
 # D 128: 176 -> 169 us; headline 14.5 -> 13.9 us after a 4 GB allocation). So every timed row
 # lets SETTLE_S pass between allocating its inputs and its warm-up calls. The headline waits idle
 # (its warm-up is the --warmup count alone); the other rows, whose warm-up is this file's choice,
-# spend the time launching the streaming-read probe over a 32 MiB buffer, since after an idle wait
+# spend the time launching the streaming-read probe over a 32 MiB buffer (128 workgroups, a grid
+# the stream ceiling does not use, so kernel traces tell the two apart), since after an idle wait
 # the clocks are down and a host-bound loop of small calls (GQA B 1, N 512) reads up to 45 % slow.
 SETTLE_S = 0.4
 _SETTLE_BUF = []
@@ -153,7 +154,7 @@ def settle(torch, fq=None):
     t_end = time.perf_counter() + SETTLE_S
     while time.perf_counter() < t_end:
         for _ in range(100):
-            fq._ext._probe_stream_read(_SETTLE_BUF[0], 256)
+            fq._ext._probe_stream_read(_SETTLE_BUF[0], 128)
         torch.cuda.synchronize()
 
 
