@@ -771,7 +771,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   const _Float16* Vsr = F::QUANT ? p.Vs + (PAGED ? 0 : (size_t)b * p.sc_bs) + (size_t)h * p.sc_hs : nullptr;
 
   const int n = lane & 15;  // column of S^T, P^T and O^T; token row of the K operand
-  const int R = lane >> 4;  // lane row: K dword group; scores and V of tokens 4R .. 4R+3
+  const int R = lane >> 4;  // lane row: K dword group; scores and V of tokens 4R .. 4R+3 (TPERM: R + 4k)
   // Column packing (cols_fold): column n carries head hh of tile jl of each
   // group of P tiles; columns past P * HG carry nothing (scores masked).
   constexpr int P = (16 / HG < U) ? 16 / HG : U;
@@ -857,17 +857,27 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   const rsrc_t rV = make_rsrc(Vr, PAGED ? 0u : (uint32_t)hi * ts);
   const rsrc_t rKs = make_rsrc(Ksr, PAGED ? 0u : (uint32_t)hi * sts);
   const rsrc_t rVs = make_rsrc(Vsr, PAGED ? 0u : (uint32_t)hi * sts);
+  // 2-byte rows (fp16, bf16): lane row R loads V tokens 4R .. 4R+3 itself (load
+  // j = token 4R + j), each load still whole row segments; narrower rows load
+  // token 4j + R (one load covers four consecutive rows) and trade chunks
+  // between lane rows afterwards (exchange_4x4). TPERM instead scores the
+  // tile's tokens transposed in groups of four (K operand row 4a + b holds
+  // token a + 4b): lane row R's score slot k is then token R + 4k, the token
+  // whose V that lane row loaded as chunk k, and P.V takes V as loaded. The K
+  // loads of a quad of lanes then touch four cache lines instead of two:
+  // int8 / fp8 one-pass waves gain (MHA B 8, N 4096, D 128 6.07 -> 5.86 us,
+  // B 32, N 512 6.40 -> 6.14 us, split-K N 512 / 4096 6.02 -> 5.83 / 7.49 ->
+  // 7.23 us), multi-pass waves and int4 lose 1-2 %.
+  constexpr bool VDIRECT = FMT == KV_F16 || FMT == KV_BF16;
+  constexpr bool TPERM = (SHORT || LAZY) && (FMT == KV_I8 || FMT == KV_FP8);
+  constexpr int TS = TPERM ? 4 : 1;  // token distance between a lane's score slots
   // K loads: operand-A layout straight from memory, or (fp16) whole rows
   // that go through the wave's LDS rows
   uint32_t koff;
   if constexpr (F::STAGE_K)
     koff = F::krow_lane(lane, ts);
   else
-    koff = (uint32_t)n * ts + F::klane(R);
-  // 2-byte rows (fp16, bf16): lane row R loads tokens 4R .. 4R+3 itself (load j
-  // = token 4R + j), each load still whole row segments; narrower rows load
-  // token 4j + R and trade chunks between lane rows afterwards (exchange_4x4)
-  constexpr bool VDIRECT = FMT == KV_F16 || FMT == KV_BF16;
+    koff = (uint32_t)(TPERM ? (n >> 2) + 4 * (n & 3) : n) * ts + F::klane(R);
   const uint32_t voff = (uint32_t)(VDIRECT ? 4 * R : R) * ts + (uint32_t)n * VG::VBYTES;
   // tile t's sources: descriptors and the byte offset of its first token
   struct TileSrc {
@@ -910,11 +920,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // its U tiles with the matrix cores (S^T: tokens on M, columns on N), keeps
   // in column n the scores of tile jl of each group of P tiles, takes ONE
   // online-softmax step over the pass, and accumulates O^T += V^T P^T on the
-  // matrix cores: the packed score layout (lane: column n, tokens 4R + k) is
+  // matrix cores: the packed score layout (lane: column n, score slots k = tokens 4R + k) is
   // operand B of the PV product of tile jl, zero for the group's other tiles,
   // so column n of O^T gathers tile jl's share of head hh.
   const int step = 16 * nw;
-  const int lane_tok = jl * step + 4 * R;  // token of the lane's first score in a group, from its base
+  const int slot0 = TPERM ? R : 4 * R;       // token of the lane's score slot 0 in its tile
+  const int lane_tok = jl * step + slot0;  // ... from the base of the lane's group of tiles
   // scales of paged rows come through per-tile descriptors: every tile's are
   // loaded and the lane's tile is picked afterwards
   constexpr bool PICK_SC = F::QUANT && PAGED && P > 1;
@@ -922,12 +933,12 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
   // 4R + 3, a multiple of 4 from lo) are one 8-byte load in passes that lie
   // wholly before hi (past the descriptor's end a load reads zeros dword by
   // dword, so a dword holding a valid and an invalid scale could lose both)
-  const bool vec_sc = F::QUANT && !PAGED && sts == 2u && (lo & 3) == 0 &&
+  const bool vec_sc = F::QUANT && !TPERM && !PAGED && sts == 2u && (lo & 3) == 0 &&
                       ((reinterpret_cast<uintptr_t>(Ksr) | reinterpret_cast<uintptr_t>(Vsr)) & 7u) == 0;
   for (int pb = lo + 16 * w; pb < hi; pb += U * step) {
     typename F::KT kr[U][F::KL];
     uint32_t vr[U][4][VD];
-    // per-token scales (int8 / int4) of tokens 4R + k of the lane's tile in group g
+    // per-token scales (int8 / int4) of the tokens of the lane's score slots k in its tile of group g
     _Float16 ks[NG][4], vs[NG][4];
     _Float16 kt[PICK_SC ? U : 1][4], vt[PICK_SC ? U : 1][4];
     TileSrc src[U];
@@ -972,7 +983,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
             const uint32_t so = (uint32_t)(pb + g * P * step) * sts;  // wave-uniform
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
-              const uint32_t vo = (uint32_t)(lane_tok + k) * sts + (F::SOFF_TILE ? 0u : so);
+              const uint32_t vo = (uint32_t)(lane_tok + TS * k) * sts + (F::SOFF_TILE ? 0u : so);
               ks[g][k] = __builtin_bit_cast(_Float16, buf_load<2>(rKs, vo, F::SOFF_TILE ? so : 0u));
               vs[g][k] = __builtin_bit_cast(_Float16, buf_load<2>(rVs, vo, F::SOFF_TILE ? so : 0u));
             }
@@ -984,7 +995,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
         for (int u = 0; u < T; ++u)
 #pragma unroll
           for (int k = 0; k < 4; ++k) {
-            const uint32_t so = src[u].soff + (uint32_t)(4 * R + k) * sts;
+            const uint32_t so = src[u].soff + (uint32_t)(slot0 + TS * k) * sts;
             const _Float16 a = __builtin_bit_cast(_Float16, buf_load<2>(src[u].ks, so));
             const _Float16 c = __builtin_bit_cast(_Float16, buf_load<2>(src[u].vs, so));
             if constexpr (PICK_SC) {
@@ -1078,7 +1089,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       for (int g = 0; g < NG; ++g)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          bool ok = pb + g * P * step + lane_tok + k < hi;
+          bool ok = pb + g * P * step + lane_tok + TS * k < hi;
           if constexpr (PAGED) ok = ok && pick<P>(jm, [&](int j) { return src[g * P + j].ok ? ~0u : 0u; }) != 0u;
           x[g][k] = ok ? x[g][k] : -INFINITY;
         }
@@ -1218,9 +1229,10 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       continue;
     }
     // Two tiles per product: v_mfma_f32_16x16x32_f16 contracts over 32
-    // operand slots, lane row R's slots 8R .. 8R+3 taking tokens 4R .. 4R+3
-    // of tile u and 8R+4 .. 8R+7 the same tokens of tile u + 1 (half the
-    // matrix-core time of two 16x16x16 products).
+    // operand slots, lane row R's slots 8R .. 8R+3 taking the tokens of its
+    // score slots (4R .. 4R+3; TPERM R, R+4, R+8, R+12) of tile u and
+    // 8R+4 .. 8R+7 the same tokens of tile u + 1 (half the matrix-core time of
+    // two 16x16x16 products).
     static_assert(U % 2 == 0, "tiles are paired");
 #pragma unroll
     for (int u = 0; u < U; u += 2) {
@@ -1235,7 +1247,7 @@ __global__ void __launch_bounds__(64 * NW_MAX) decode_partial_kernel(PartialPara
       auto wts = [&](int t, h4_t& bh, h4_t& bl) {
 #pragma unroll
         for (int dw = 0; dw < VD; ++dw) {
-          if constexpr (!VDIRECT) exchange_4x4(vr[t][0][dw], vr[t][1][dw], vr[t][2][dw], vr[t][3][dw]);
+          if constexpr (!VDIRECT && !TPERM) exchange_4x4(vr[t][0][dw], vr[t][1][dw], vr[t][2][dw], vr[t][3][dw]);
 #pragma unroll
           for (int j = 0; j < 4; ++j) vr[t][j][dw] = F::vprep(vr[t][j][dw]);
         }
