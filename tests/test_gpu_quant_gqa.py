@@ -150,3 +150,39 @@ def test_quantized_entry_points_reject_bad_input():
         fq.decode_attn_gqa_int8(q, K, K, s[:, :1], s[:, :1], 8)
     with pytest.raises(RuntimeError, match="^heads"):
         fq.decode_attn_gqa_int8(draw(g, 1, 7, 128).half().cuda(), K, K, s, s, 8)
+
+
+@pytest.mark.parametrize("fmt", ["int8", "fp8"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("N,S,W", [(17, 1, 8), (100, 3, 8), (257, 8, 4), (1000, 16, 8), (2047, 32, 8),
+                                   (4100, 32, 8), (16383, 32, 8), (129, 2, 2)])
+def test_one_pass_waves_transposed_tokens_ragged(fmt, D, N, S, W, merge_mode):
+    """int8 / fp8 waves of one pass (two-tile passes, and one four-tile pass with
+    the deferred query preparation) score their tiles in a transposed token order
+    and take V as loaded: splits and rows that end inside a tile, output and
+    split scratch against the oracle, for grouped (Hq 32 / Hkv 8) heads."""
+    g = torch.Generator().manual_seed(53 + N + D)
+    Hq, Hkv = 32, 8
+    q = draw(g, Hq, D).half()
+    if fmt == "int8":
+        Kq, Ks, Kf = quantized("int8", draw(g, Hkv, N, D))
+        Vq, Vs, Vf = quantized("int8", draw(g, Hkv, N, D))
+        f = fq.gqa_sk_fast_int8
+    else:
+        Kq, Ks = fq.quantize_fp8_per_token(draw(g, Hkv, N, D).cuda())
+        Vq, Vs = fq.quantize_fp8_per_token(draw(g, Hkv, N, D).cuda())
+        codes = lambda t: t.view(torch.uint8).cpu().numpy()
+        Kf = oracle.dequant_fp8(codes(Kq), Ks.cpu().numpy())
+        Vf = oracle.dequant_fp8(codes(Vq), Vs.cpu().numpy())
+        f = fq.gqa_sk_fast_fp8
+    mp = torch.empty(Hq, S, device="cuda")
+    lp = torch.empty(Hq, S, device="cuda")
+    op = torch.empty(Hq, S, D, device="cuda")
+    o = torch.empty(Hq, D, device="cuda", dtype=torch.float16)
+    f(q.cuda(), Kq, Vq, Ks, Vs, mp, lp, op, o, S, W, 8)
+    assert maxerr(o, oracle.gqa_attention(q.numpy()[None], Kf[None], Vf[None])[0]) <= TOL
+    if S > 1:
+        m, l, acc = oracle.split_partials(q.numpy(), Kf, Vf, S)
+        assert np.array_equal(np.isneginf(mp.cpu().numpy()), np.isneginf(m))
+        np.testing.assert_allclose(lp.cpu().numpy(), l, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(op.cpu().numpy(), acc, rtol=1e-4, atol=2e-4)
