@@ -22,8 +22,8 @@ on CPU tensors, every host thread) on a bounded sample of the same workload.
 Further keys carry the reference's other benchmark shapes: MHA fp16 / int8 /
 int4 at B=2048, N=4096, D=128; split-K at B=8, N=32768; the launch floor; the
 reference's primary split-K table (D in {64, 128} x N in {512 .. 32768}, each
-point swept over S/W/CW under the correctness gate); the remaining BASELINE
-rows at D=128 (MHA B=32 N=512; fp16 / int8 / int4 MHA at B=8 and 256; GQA at
+point swept over S/W/CW under the correctness gate); the reference's other
+benchmark rows at D=128 (MHA B=32 N=512; fp16 / int8 / int4 MHA at B=8 and 256; GQA at
 N=512, D=64 against repeat_kv + MHA; int8 / int4 split-K at the headline
 shape); and the reference's D=64 tables with its A100 numbers alongside.
 
@@ -1223,7 +1223,8 @@ def splitk_primary_table(torch, fq, sweep_steps=200, sweep_warmup=20, steps=2000
 
 
 def baseline_rows(torch, fq):
-    """BASELINE.md section 2 rows beside the headline, the B = 2048 MHA rows and the primary table:
+    """The reference's other benchmark rows at D = 128, beside the headline, the B = 2048 MHA rows
+    and the primary table:
     * mha_fp16_b32_n512_d128: fp16 MHA, 32 heads, N 512, D 128 (the reference's CPU-runnable case);
     * mha_n4096_d128: fp16 / int8 / int4 MHA at B 8 and 256, N 4096, D 128 (B 2048 is
       mha_b2048_n4096_d128);
@@ -1366,7 +1367,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the secondary keys (MHA B=2048, split-K B=8 N=32K, launch floor, primary "
-                         "split-K table, BASELINE rows, the reference's D=64 tables)")
+                         "split-K table, the other D=128 rows, the reference's D=64 tables)")
     ap.add_argument("--suite", metavar="FILE", default="",
                     help="also measure the secondary configurations, JSON lines into FILE")
     ap.add_argument("--suite-only", metavar="NAMES", default=",".join(SUITES),
