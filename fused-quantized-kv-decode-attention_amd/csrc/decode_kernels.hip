@@ -28,7 +28,10 @@
 //      bf16 lanes load their own four tokens' row segments; narrower rows
 //      load four consecutive rows per instruction and a 4 x 4 exchange of
 //      the V chunks between lane rows and registers (v_permlane32_swap /
-//      v_permlane16_swap) regroups them; int8/int4 become exact fp16 on the
+//      v_permlane16_swap) regroups them (int8 / fp8 waves of one pass instead
+//      score each group of four tokens in transposed order, so the tokens a
+//      lane row scores are the ones whose V it loaded, and skip the exchange);
+//      int8/int4 become exact fp16 on the
 //      way. Each tile's weights enter operand B in the columns
 //      0 .. HG-1 that are emitted (fp16: moved there by a DPP row shift) or
 //      in the tile's own columns, the rest zero, summed at the end (int8 /
